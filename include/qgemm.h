@@ -1,0 +1,144 @@
+/*
+ * qgemm.h — C ABI of the MI355X (gfx950) quantized-weight GEMM library
+ * (librdna2_qgemm.so).
+ *
+ * Conventions (mirroring the reference's only native ABI,
+ * rdna2-ops/rdna2_ops/csrc/group_norm_silu.hip:283-321, loaded by ctypes in
+ * rdna2-ops/rdna2_ops/normalization.py:16-27):
+ *   - every entry point returns an int that is a hipError_t value; 0 = success;
+ *   - bad arguments return hipErrorInvalidValue (1) BEFORE any HIP call, so
+ *     argument validation is testable without a GPU;
+ *   - all pointers are device pointers owned by the caller; outputs and
+ *     workspace are allocated by the caller (query *_workspace_bytes first);
+ *   - launches are asynchronous on `stream` (a hipStream_t, NULL = default);
+ *   - the library allocates nothing, never synchronises and keeps no mutable
+ *     global state; concurrent calls need distinct workspace;
+ *   - strides are in ELEMENTS of the tensor they describe;
+ *   - dtype codes: QG_F32 = 0, QG_F16 = 1, QG_BF16 = 2 (same numbering as
+ *     normalization.py:14), then QG_I32, QG_I8, QG_U8, QG_E4M3, QG_E5M2.
+ */
+#ifndef RDNA2_QGEMM_H
+#define RDNA2_QGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum qg_dtype {
+  QG_F32 = 0,
+  QG_F16 = 1,
+  QG_BF16 = 2,
+  QG_I32 = 3,
+  QG_I8 = 4,
+  QG_U8 = 5,
+  QG_E4M3 = 6, /* OCP float8 e4m3fn (torch.float8_e4m3fn) */
+  QG_E5M2 = 7  /* OCP float8 e5m2 (torch.float8_e5m2) */
+};
+
+/* Epilogue flags of the INT8 GEMM (bit field). */
+enum qg_epilogue {
+  /* order F (default, 0): v = f32(acc) * (sa[m] * sb[n]); v = v + f32(bias[n]);
+   *   act(v); one RNE rounding to out dtype.  int8_gemm.py:53-63, :191. */
+  QG_EPI_ORDER_FUSED_FMA = 1, /* rounding="fused": v = fma(f32(acc), sa*sb, bias)
+                                 (int8_gemm.py:191 enable_fp_fusion=True) */
+  QG_EPI_ORDER_EAGER = 2,     /* Kitchen eager order E: t = out(f32(acc)*(sa*sb));
+                                 t = out(f32(t) + f32(out(bias))) (comfy_int8.py:128-143) */
+  QG_EPI_GELU_TANH = 4        /* GELU(tanh approximation) in fp32 before the final
+                                 rounding (new) */
+};
+
+/* Rounding mode of the per-row INT8 quantizer. */
+enum qg_rounding {
+  QG_ROUND_HALF_EVEN = 0, /* q = rint(x / step)        (BASELINE: round-half-even) */
+  QG_ROUND_HALF_AWAY = 1  /* q = floor(z+.5) | ceil(z-.5) (fp8_weight_gemm_v06.py:87-90) */
+};
+
+/* W4 storage flags (bit field). */
+enum qg_w4_flags {
+  QG_W4_SIGNED_NIBBLES = 1, /* stored nibble = q & 15 with q in [-8,7] and int32
+                               zero points in the same signed coordinates
+                               (reference PackedInt4, int4_weight_gemm_v07.py:49-82);
+                               otherwise nibble and zero point are unsigned uint4 */
+  QG_W4_ORDER_HIGH = 2,     /* nibble i of a word at bits 28-4i (order="high") */
+  QG_W4_LAYOUT_KN = 4,      /* words are [K/8, N] (layout="kn") instead of [N, K/8] */
+  QG_W4_ZEROS_PACKED = 8    /* zero points are uint4 packed 8 per int32 along the
+                               group axis, [N, ceil(G/8)]; else int32 [N, G] */
+};
+
+/* Error string of a returned status. Mirrors rdna2_hip_error_string
+ * (group_norm_silu.hip:319-321). */
+const char* qg_error_string(int status);
+
+/* Library build identity: "gfx950 <git-less source digest>". */
+const char* qg_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Per-row dynamic INT8 quantizer.
+ * Replaces: Kitchen eager.quantize_int8_rowwise (third-party comfy_kitchen
+ *   0.2.40, called at rdna2-ops/rdna2_ops/comfy_int8.py:122 and
+ *   int8_gemm.py:255) and the in-tree Triton _quant_rows
+ *   (rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:76-92).
+ * step[m] = max(absmax(x[m,:]) / 127, 1e-20) (IEEE fp32 division);
+ * q[m,k] = clamp(round(x[m,k] / step[m]), -127, 127) with IEEE division.
+ * x_dtype: QG_F32 / QG_F16 / QG_BF16 / QG_E4M3 / QG_E5M2 (fp8 decoded exactly
+ * first, as fp8_weight_gemm_v06.py:83-84). q is [m, k] with row stride q_sm.
+ * ------------------------------------------------------------------------- */
+int qg_quant_rows_i8(const void* x, int x_dtype, int64_t x_sm, int64_t x_sk,
+                     int64_t m, int64_t k, int8_t* q, int64_t q_sm, float* step,
+                     int rounding, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * INT8 x INT8 -> INT32 GEMM with an optional fused dequant epilogue.
+ * Replaces: _int8_dot_dequant / _int8_dot_dequant_wrapped + _launch
+ *   (rdna2-ops/rdna2_ops/int8_gemm.py:19-123, :152-192), i.e. the entry
+ *   points int8_matmul (:195-200) and int8_gemm_dequant (:203-214).
+ * a: [m, k] int8 with strides (a_sm, a_sk); b: [k, n] int8 with strides
+ * (b_sk, b_sn) — the MOSS call passes weight.T, i.e. b_sk = 1, b_sn = k.
+ * a_scale == NULL: integer GEMM, out_dtype must be QG_I32.
+ * Otherwise a_scale: [m] fp32, b_scale: [n] fp32 (b_scale_numel == n) or a
+ * scalar (b_scale_numel == 1); bias: NULL or [n] of bias_dtype
+ * (QG_F32/QG_F16/QG_BF16); out_dtype QG_F32 / QG_F16 / QG_BF16.
+ * out: [m, n] contiguous. Non-canonical strides or k % 64 != 0 are packed into
+ * the workspace first (see qg_int8_gemm_workspace_bytes).
+ * k must be <= 131071 (int8_gemm.py:142-143).
+ * ------------------------------------------------------------------------- */
+size_t qg_int8_gemm_workspace_bytes(const void* a, int64_t a_sm, int64_t a_sk,
+                                    const void* b, int64_t b_sk, int64_t b_sn,
+                                    int64_t m, int64_t n, int64_t k);
+int qg_int8_gemm(const int8_t* a, int64_t a_sm, int64_t a_sk, const int8_t* b,
+                 int64_t b_sk, int64_t b_sn, int64_t m, int64_t n, int64_t k,
+                 const float* a_scale, const float* b_scale,
+                 int64_t b_scale_numel, const void* bias, int bias_dtype,
+                 void* out, int out_dtype, int epilogue, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * W8A8 linear: per-token activation quantize prologue + INT8 GEMM + epilogue
+ * in one call: out = epi(quant(x) @ w.T).
+ * Replaces: the MOSS candidate body quantize_int8_rowwise -> int8_gemm_dequant
+ *   (rdna2-ops/rdna2_ops/int8_gemm.py:254-259) and the FP8 "int8" method
+ *   (fp8_weight_gemm_v06.py:181-193).
+ * x: [m, k] (x_dtype QG_F32/QG_F16/QG_BF16, row stride x_sm, unit k stride);
+ * w: [n, k] int8 row-major (row stride w_sn); w_scale [n] or scalar.
+ * The workspace holds the int8 activations ([m, round_up(k, 64)]), their fp32
+ * steps ([m]) and, when w is not canonical ([n, k] with unit k stride,
+ * 16-byte aligned rows and k % 64 == 0), a zero-padded packed copy of w; its
+ * size comes from qg_w8a8_linear_workspace_bytes.
+ * ------------------------------------------------------------------------- */
+size_t qg_w8a8_linear_workspace_bytes(const int8_t* w, int64_t w_sn, int64_t m,
+                                      int64_t n, int64_t k);
+int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t m,
+                   int64_t k, const int8_t* w, int64_t w_sn, int64_t n,
+                   const float* w_scale, int64_t w_scale_numel,
+                   const void* bias, int bias_dtype, void* out, int out_dtype,
+                   int rounding, int epilogue, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RDNA2_QGEMM_H */

@@ -1,0 +1,235 @@
+// extern "C" entry points of librdna2_qgemm.so (declared in include/qgemm.h).
+//
+// Argument validation happens here, before any HIP call, and returns
+// hipErrorInvalidValue like the reference's native ABI
+// (rdna2-ops/rdna2_ops/csrc/group_norm_silu.hip:298-317). The library never
+// allocates: non-canonical operands are packed into caller workspace.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qgemm.h"
+#include "qg_internal.h"
+
+namespace {
+
+constexpr int64_t kMaxK = 131071;  // int32 accumulator bound, int8_gemm.py:142-143
+constexpr int64_t kIntMax = 2147483647;
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// A [m, k] (strides a_sm, a_sk) can be read in place by the GEMM kernel.
+inline bool canonical_rows(const void* p, int64_t s_row, int64_t s_k, int64_t rows, int64_t k) {
+  (void)rows;
+  return s_k == 1 && (s_row % 16) == 0 && aligned16(p) && (k % 64) == 0;
+}
+
+inline bool float_dtype(int d) { return d == QG_F32 || d == QG_F16 || d == QG_BF16; }
+
+struct I8Plan {
+  bool pack_a, pack_b;
+  int64_t kp;
+  size_t a_bytes, b_bytes;
+  size_t total() const { return a_bytes + b_bytes; }
+};
+
+I8Plan plan_i8(const void* a, int64_t a_sm, int64_t a_sk, const void* b, int64_t b_sk,
+               int64_t b_sn, int64_t m, int64_t n, int64_t k) {
+  I8Plan pl;
+  pl.kp = round_up(k, 64);
+  // B = W^T: W [n, k] has row stride b_sn and element stride b_sk.
+  pl.pack_a = !canonical_rows(a, a_sm, a_sk, m, k);
+  pl.pack_b = !canonical_rows(b, b_sn, b_sk, n, k);
+  pl.a_bytes = pl.pack_a ? static_cast<size_t>(round_up(m * pl.kp, 256)) : 0;
+  pl.b_bytes = pl.pack_b ? static_cast<size_t>(round_up(n * pl.kp, 256)) : 0;
+  return pl;
+}
+
+bool valid_epilogue(int epi) {
+  if (epi & ~(QG_EPI_ORDER_FUSED_FMA | QG_EPI_ORDER_EAGER | QG_EPI_GELU_TANH)) return false;
+  if ((epi & QG_EPI_ORDER_EAGER) && (epi & (QG_EPI_ORDER_FUSED_FMA | QG_EPI_GELU_TANH))) return false;
+  return true;
+}
+
+bool valid_gemm_shape(int64_t m, int64_t n, int64_t k, int64_t a_sm, int64_t a_sk, int64_t b_sk,
+                      int64_t b_sn) {
+  if (m < 0 || n < 0 || k < 0 || k > kMaxK || m > kIntMax || n > kIntMax) return false;
+  if (a_sm < 0 || a_sk < 0 || b_sk < 0 || b_sn < 0) return false;
+  if (m * n > (int64_t(1) << 40)) return false;
+  return true;
+}
+
+}  // namespace
+
+extern "C" const char* qg_error_string(int status) {
+  return hipGetErrorString(static_cast<hipError_t>(status));
+}
+
+extern "C" const char* qg_version(void) { return "librdna2_qgemm gfx950 1"; }
+
+extern "C" int qg_quant_rows_i8(const void* x, int x_dtype, int64_t x_sm, int64_t x_sk, int64_t m,
+                                int64_t k, int8_t* q, int64_t q_sm, float* step, int rounding,
+                                void* stream) {
+  if (m < 0 || k < 0 || m > kIntMax || k > kIntMax || x_sm < 0 || x_sk < 0 || q_sm < k)
+    return hipErrorInvalidValue;
+  if (!(float_dtype(x_dtype) || x_dtype == QG_E4M3 || x_dtype == QG_E5M2)) return hipErrorInvalidValue;
+  if (rounding != QG_ROUND_HALF_EVEN && rounding != QG_ROUND_HALF_AWAY) return hipErrorInvalidValue;
+  if (m == 0) return hipSuccess;
+  if (!q || !step || (k > 0 && !x)) return hipErrorInvalidValue;
+  return qg::launch_quant_rows(x, x_dtype, x_sm, x_sk, m, k, q, q_sm, k, step, rounding,
+                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t qg_int8_gemm_workspace_bytes(const void* a, int64_t a_sm, int64_t a_sk,
+                                               const void* b, int64_t b_sk, int64_t b_sn,
+                                               int64_t m, int64_t n, int64_t k) {
+  if (!valid_gemm_shape(m, n, k, a_sm, a_sk, b_sk, b_sn)) return 0;
+  return plan_i8(a, a_sm, a_sk, b, b_sk, b_sn, m, n, k).total();
+}
+
+namespace {
+
+int int8_gemm_impl(const int8_t* a, int64_t a_sm, int64_t a_sk, const int8_t* b, int64_t b_sk,
+                   int64_t b_sn, int64_t m, int64_t n, int64_t k, const float* a_scale,
+                   const float* b_scale, int64_t b_scale_numel, const void* bias, int bias_dtype,
+                   void* out, int out_dtype, int epilogue, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
+  if (!valid_gemm_shape(m, n, k, a_sm, a_sk, b_sk, b_sn)) return hipErrorInvalidValue;
+  if (!valid_epilogue(epilogue)) return hipErrorInvalidValue;
+  const bool dequant = a_scale != nullptr;
+  if (dequant) {
+    if (!float_dtype(out_dtype)) return hipErrorInvalidValue;
+    if (!b_scale || (b_scale_numel != 1 && b_scale_numel != n)) return hipErrorInvalidValue;
+    if (bias && !float_dtype(bias_dtype)) return hipErrorInvalidValue;
+  } else {
+    if (out_dtype != QG_I32 || b_scale || bias || epilogue != 0) return hipErrorInvalidValue;
+  }
+  if (m == 0 || n == 0) return hipSuccess;
+  if (!out || (k > 0 && (!a || !b))) return hipErrorInvalidValue;
+  const I8Plan pl = plan_i8(a, a_sm, a_sk, b, b_sk, b_sn, m, n, k);
+  if (pl.total() > 0 && (!workspace || workspace_bytes < pl.total() || !aligned16(workspace)))
+    return hipErrorInvalidValue;
+
+  qg::I8GemmArgs p{};
+  p.M = static_cast<int>(m);
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(pl.kp);
+  char* ws = static_cast<char*>(workspace);
+  if (pl.pack_a) {
+    int8_t* pa = reinterpret_cast<int8_t*>(ws);
+    hipError_t e = qg::launch_pack_rows_i8(a, a_sm, a_sk, m, k, pa, pl.kp, stream);
+    if (e != hipSuccess) return e;
+    p.a = pa;
+    p.a_sm = pl.kp;
+  } else {
+    p.a = a;
+    p.a_sm = a_sm;
+  }
+  if (pl.pack_b) {
+    int8_t* pb = reinterpret_cast<int8_t*>(ws + pl.a_bytes);
+    hipError_t e = qg::launch_pack_rows_i8(b, b_sn, b_sk, n, k, pb, pl.kp, stream);
+    if (e != hipSuccess) return e;
+    p.w = pb;
+    p.w_sn = pl.kp;
+  } else {
+    p.w = b;
+    p.w_sn = b_sn;
+  }
+  p.a_scale = a_scale;
+  p.b_scale = b_scale;
+  p.b_scalar = b_scale_numel == 1;
+  p.bias = bias;
+  p.bias_dtype = bias_dtype;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  p.epi = epilogue;
+  return qg::launch_i8_gemm(p, stream);
+}
+
+}  // namespace
+
+extern "C" int qg_int8_gemm(const int8_t* a, int64_t a_sm, int64_t a_sk, const int8_t* b,
+                            int64_t b_sk, int64_t b_sn, int64_t m, int64_t n, int64_t k,
+                            const float* a_scale, const float* b_scale, int64_t b_scale_numel,
+                            const void* bias, int bias_dtype, void* out, int out_dtype,
+                            int epilogue, void* workspace, size_t workspace_bytes, void* stream) {
+  return int8_gemm_impl(a, a_sm, a_sk, b, b_sk, b_sn, m, n, k, a_scale, b_scale, b_scale_numel,
+                        bias, bias_dtype, out, out_dtype, epilogue, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(stream));
+}
+
+namespace {
+// Workspace of the W8A8 linear: int8 activations [m, kp], fp32 steps [m], then
+// a packed copy of W when W is not canonical ([n, k] row-major, 16-byte rows,
+// k % 64 == 0).
+struct W8A8Plan {
+  int64_t kp;
+  size_t act_bytes, step_bytes;
+  I8Plan w;
+  size_t total() const { return act_bytes + step_bytes + w.b_bytes; }
+};
+W8A8Plan plan_w8a8(const void* w, int64_t w_sn, int64_t m, int64_t n, int64_t k) {
+  W8A8Plan pl;
+  pl.kp = round_up(k, 64);
+  pl.act_bytes = static_cast<size_t>(round_up(m * pl.kp, 256));
+  pl.step_bytes = static_cast<size_t>(round_up(m * 4, 256));
+  pl.w = plan_i8(nullptr, pl.kp, 1, w, 1, w_sn, m, n, k);
+  pl.w.a_bytes = 0;
+  return pl;
+}
+}  // namespace
+
+extern "C" size_t qg_w8a8_linear_workspace_bytes(const int8_t* w, int64_t w_sn, int64_t m,
+                                                 int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k < 0 || k > kMaxK || w_sn < 0) return 0;
+  return plan_w8a8(w, w_sn, m, n, k).total();
+}
+
+extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t k,
+                              const int8_t* w, int64_t w_sn, int64_t n, const float* w_scale,
+                              int64_t w_scale_numel, const void* bias, int bias_dtype, void* out,
+                              int out_dtype, int rounding, int epilogue, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (m < 0 || n < 0 || k < 0 || k > kMaxK || x_sm < 0 || w_sn < 0) return hipErrorInvalidValue;
+  if (m > kIntMax || n > kIntMax || m * n > (int64_t(1) << 40)) return hipErrorInvalidValue;
+  if (!float_dtype(x_dtype) || !float_dtype(out_dtype)) return hipErrorInvalidValue;
+  if (rounding != QG_ROUND_HALF_EVEN && rounding != QG_ROUND_HALF_AWAY) return hipErrorInvalidValue;
+  if (!valid_epilogue(epilogue)) return hipErrorInvalidValue;
+  if (!w_scale || (w_scale_numel != 1 && w_scale_numel != n)) return hipErrorInvalidValue;
+  if (bias && !float_dtype(bias_dtype)) return hipErrorInvalidValue;
+  if (m == 0 || n == 0) return hipSuccess;
+  if (!out || (k > 0 && (!x || !w))) return hipErrorInvalidValue;
+  const W8A8Plan pl = plan_w8a8(w, w_sn, m, n, k);
+  if (!workspace || workspace_bytes < pl.total() || !aligned16(workspace)) return hipErrorInvalidValue;
+  char* ws = static_cast<char*>(workspace);
+  int8_t* xq = reinterpret_cast<int8_t*>(ws);
+  float* xs = reinterpret_cast<float*>(ws + pl.act_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = qg::launch_quant_rows(x, x_dtype, x_sm, 1, m, k, xq, pl.kp, pl.kp, xs, rounding, s);
+  if (e != hipSuccess) return e;
+  qg::I8GemmArgs p{};
+  p.M = static_cast<int>(m);
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(pl.kp);
+  p.a = xq;
+  p.a_sm = pl.kp;
+  if (pl.w.pack_b) {
+    int8_t* pw = reinterpret_cast<int8_t*>(ws + pl.act_bytes + pl.step_bytes);
+    e = qg::launch_pack_rows_i8(w, w_sn, 1, n, k, pw, pl.kp, s);
+    if (e != hipSuccess) return e;
+    p.w = pw;
+    p.w_sn = pl.kp;
+  } else {
+    p.w = w;
+    p.w_sn = w_sn;
+  }
+  p.a_scale = xs;
+  p.b_scale = w_scale;
+  p.b_scalar = w_scale_numel == 1;
+  p.bias = bias;
+  p.bias_dtype = bias_dtype;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  p.epi = epilogue;
+  return qg::launch_i8_gemm(p, s);
+}

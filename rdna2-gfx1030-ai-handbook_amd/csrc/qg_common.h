@@ -1,0 +1,138 @@
+// Shared device helpers for the gfx950 quantized-GEMM kernels.
+//
+// Every file of this library is compiled for gfx950 only (wave64, CDNA4 MFMA,
+// 160 KB LDS per CU) with -ffp-contract=off so that the fp32 epilogues keep
+// the reference's separate multiply/add rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "../../include/qgemm.h"
+
+namespace qg {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+// fp32 -> bf16 with round-to-nearest-even (NaN stays a quiet NaN); the same
+// rule as c10::BFloat16's round_to_nearest_even.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+// fp32 -> fp16, hardware conversion (round-to-nearest-even, fp16 denormals kept).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Exact decode of an OCP fp8 byte to fp32, bit for bit the construction of the
+// reference decoder (rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:21-37):
+// e4m3fn: exponent 0 -> m * 2^-9; 0x7f / 0xff -> NaN; else (e+120)<<23 | m<<20.
+// e5m2:   exponent 0 -> m * 2^-16; exponent 31 -> inf / NaN; else (e+112)<<23 | m<<21.
+__device__ __forceinline__ float fp8_to_f32(uint32_t u, bool e5) {
+  const uint32_t sign = (u & 128u) << 24;
+  uint32_t bits;
+  if (e5) {
+    const uint32_t e = (u >> 2) & 31u, m = u & 3u;
+    bits = ((e + 112u) << 23) | (m << 21);
+    if (e == 0) bits = __float_as_uint(static_cast<float>(m) * 0.0000152587890625f);
+    if (e == 31) bits = 0x7f800000u | (m << 21);
+  } else {
+    const uint32_t e = (u >> 3) & 15u, m = u & 7u;
+    bits = ((e + 120u) << 23) | (m << 20);
+    if (e == 0) bits = __float_as_uint(static_cast<float>(m) * 0.001953125f);
+    if (e == 15 && m == 7) bits = 0x7fc00000u;
+  }
+  return __uint_as_float(bits | sign);
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E). Used
+// where every index into a register array must be a constant, independent of
+// the unroller's size heuristics (a dynamic index sends the array to scratch).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+template <typename T>
+__host__ __device__ __forceinline__ T ceil_div(T a, T b) { return (a + b - 1) / b; }
+
+// Wave-wide reductions (wave64).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Direct global -> LDS copy of 16 bytes per lane (gfx950 global_load_lds_dwordx4).
+// The 64 lanes of the wave write 1 KB of LDS: lane i writes bytes
+// [lds_addr + 16 i, lds_addr + 16 i + 16). lds_addr must be wave-uniform.
+// Issued through inline assembly so that the compiler does not add its own
+// conservative vmcnt(0) waits before later LDS reads; the caller waits with
+// wait_vm_barrier<N>() instead. M0 is saved and restored around the load.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(gptr)
+      : "memory");
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight
+// (loads complete in order), drain LDS reads, then barrier the workgroup.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 1) asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 5) asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 7) asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 10) asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 14) asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 18) asm volatile("s_waitcnt vmcnt(18) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 20) asm volatile("s_waitcnt vmcnt(20) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 21) asm volatile("s_waitcnt vmcnt(21) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 24) asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 28) asm volatile("s_waitcnt vmcnt(28) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 32) asm volatile("s_waitcnt vmcnt(32) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else static_assert(N == 0, "add the vmcnt immediate to wait_vm_barrier");
+}
+
+// 32-bit LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+  return static_cast<uint32_t>(
+      (uintptr_t)((const __attribute__((address_space(3))) char*)(p)));
+}
+
+}  // namespace qg

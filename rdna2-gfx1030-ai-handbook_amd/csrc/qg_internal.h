@@ -1,0 +1,40 @@
+// Host-side launch interface shared by the translation units of the library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qg {
+
+// Canonical INT8 GEMM operands: A [M, K] and W [N, K] (B = W^T), both with
+// unit K stride, 16-byte aligned rows and K % 64 == 0 (zero padded).
+struct I8GemmArgs {
+  const int8_t* a;
+  int64_t a_sm;
+  const int8_t* w;
+  int64_t w_sn;
+  int M, N, K;
+  const float* a_scale;  // nullptr: int32 output
+  const float* b_scale;
+  int b_scalar;
+  const void* bias;      // nullptr or [N] of bias_dtype
+  int bias_dtype;
+  void* out;             // [M, N] contiguous
+  int out_dtype;
+  int epi;
+};
+
+hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream);
+
+// dst[r, k] = src[r * s_r + k * s_k] for k < K, 0 for K <= k < k_pad.
+hipError_t launch_pack_rows_i8(const int8_t* src, int64_t s_r, int64_t s_k,
+                               int64_t rows, int64_t K, int8_t* dst,
+                               int64_t k_pad, hipStream_t stream);
+
+// Per-row INT8 quantizer; columns [K, k_pad) of q are written as zeros.
+hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t x_sm,
+                             int64_t x_sk, int64_t M, int64_t K, int8_t* q,
+                             int64_t q_sm, int64_t k_pad, float* step,
+                             int rounding, hipStream_t stream);
+
+}  // namespace qg

@@ -1,0 +1,178 @@
+// Per-row dynamic INT8 quantizer and the strided int8 row packer.
+//
+// quant: one wave per row (rows are at most a few tens of KB, so a wave keeps
+// 64 x 16-byte loads in flight and needs no workgroup-level reduction).
+//   pass 1: absmax over the row (16-byte vector loads when the row allows);
+//   step = max(absmax / 127, 1e-20)          (IEEE fp32 division)
+//   pass 2: q = clamp(round(x / step), -127, 127) with IEEE division, the row
+//           is re-read from L2 (it was just streamed), so HBM sees it once.
+// The step formula and the half-away rounding follow the reference's
+// in-tree quantizer rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:76-92; the
+// half-even mode is the BASELINE per-token rule (absmax/127, round-half-even).
+#include "qg_common.h"
+#include "qg_internal.h"
+
+namespace qg {
+
+namespace {
+
+template <int XT>
+struct XType;
+template <> struct XType<QG_F32> { static constexpr int size = 4; };
+template <> struct XType<QG_F16> { static constexpr int size = 2; };
+template <> struct XType<QG_BF16> { static constexpr int size = 2; };
+template <> struct XType<QG_E4M3> { static constexpr int size = 1; };
+template <> struct XType<QG_E5M2> { static constexpr int size = 1; };
+
+template <int XT>
+__device__ __forceinline__ float load_x(const char* base, int64_t idx) {
+  if constexpr (XT == QG_F32) return reinterpret_cast<const float*>(base)[idx];
+  else if constexpr (XT == QG_F16) return f16_to_f32(reinterpret_cast<const uint16_t*>(base)[idx]);
+  else if constexpr (XT == QG_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[idx]);
+  else return fp8_to_f32(reinterpret_cast<const uint8_t*>(base)[idx], XT == QG_E5M2);
+}
+
+// Decode the 16/size elements of one 16-byte chunk.
+template <int XT>
+__device__ __forceinline__ void decode_chunk(const i32x4 c, float* v) {
+  constexpr int E = 16 / XType<XT>::size;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const uint32_t word = static_cast<uint32_t>(c[(e * XType<XT>::size) / 4]);
+    if constexpr (XT == QG_F32) v[e] = __uint_as_float(word);
+    else if constexpr (XT == QG_F16) v[e] = f16_to_f32(static_cast<uint16_t>(word >> (16 * (e & 1))));
+    else if constexpr (XT == QG_BF16) v[e] = bf16_to_f32(static_cast<uint16_t>(word >> (16 * (e & 1))));
+    else v[e] = fp8_to_f32((word >> (8 * (e & 3))) & 0xffu, XT == QG_E5M2);
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ int quant_one(float x, float step) {
+#pragma clang fp contract(off)
+  const float z = __fdiv_rn(x, step);
+  float q;
+  if constexpr (MODE == QG_ROUND_HALF_EVEN) {
+    q = __builtin_rintf(z);
+  } else {
+    q = z >= 0.0f ? floorf(z + 0.5f) : ceilf(z - 0.5f);
+  }
+  q = fminf(fmaxf(q, -127.0f), 127.0f);
+  return static_cast<int>(q);
+}
+
+template <int XT, int MODE, bool VEC>
+__global__ __launch_bounds__(256) void k_quant_rows(const char* x, int64_t x_sm, int64_t x_sk,
+                                                    int M, int K, int8_t* q, int64_t q_sm,
+                                                    int k_pad, float* step_out) {
+#pragma clang fp contract(off)
+  constexpr int ES = XType<XT>::size;
+  constexpr int E = 16 / ES;  // elements per 16-byte chunk
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const char* xr = x + static_cast<int64_t>(row) * x_sm * ES;
+  int8_t* qr = q + static_cast<int64_t>(row) * q_sm;
+
+  float amax = 0.0f;
+  if constexpr (VEC) {
+    const int chunks = K / E;
+    for (int c = lane; c < chunks; c += 64) {
+      const i32x4 raw = reinterpret_cast<const i32x4*>(xr)[c];
+      float v[E];
+      decode_chunk<XT>(raw, v);
+#pragma unroll
+      for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    }
+  } else {
+    for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(load_x<XT>(xr, k * x_sk)));
+  }
+  amax = wave_max(amax);
+  const float step = fmaxf(amax / 127.0f, 1.0e-20f);
+
+  if constexpr (VEC) {
+    const int chunks = K / E;
+    for (int c = lane; c < chunks; c += 64) {
+      const i32x4 raw = reinterpret_cast<const i32x4*>(xr)[c];
+      float v[E];
+      decode_chunk<XT>(raw, v);
+      uint32_t packed[E / 4 > 0 ? E / 4 : 1] = {};
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        packed[e / 4] |= (static_cast<uint32_t>(quant_one<MODE>(v[e], step)) & 0xffu) << (8 * (e & 3));
+      if constexpr (E == 4) reinterpret_cast<uint32_t*>(qr)[c] = packed[0];
+      else if constexpr (E == 8) reinterpret_cast<uint2*>(qr)[c] = make_uint2(packed[0], packed[1]);
+      else reinterpret_cast<uint4*>(qr)[c] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    }
+  } else {
+    for (int k = lane; k < K; k += 64)
+      qr[k] = static_cast<int8_t>(quant_one<MODE>(load_x<XT>(xr, k * x_sk), step));
+  }
+  for (int k = K + lane; k < k_pad; k += 64) qr[k] = 0;
+  if (lane == 0) step_out[row] = step;
+}
+
+template <int XT, int MODE>
+hipError_t launch_quant_t(const void* x, int64_t x_sm, int64_t x_sk, int64_t M, int64_t K,
+                          int8_t* q, int64_t q_sm, int64_t k_pad, float* step, hipStream_t stream) {
+  constexpr int ES = XType<XT>::size;
+  constexpr int E = 16 / ES;
+  const uintptr_t xa = reinterpret_cast<uintptr_t>(x), qa = reinterpret_cast<uintptr_t>(q);
+  const bool vec = x_sk == 1 && (xa % 16) == 0 && ((x_sm * ES) % 16) == 0 && (K % E) == 0 &&
+                   (qa % E) == 0 && (q_sm % E) == 0;
+  const dim3 grid(static_cast<unsigned>(ceil_div<int64_t>(M, 4)));
+  const char* xp = static_cast<const char*>(x);
+  if (vec)
+    hipLaunchKernelGGL((k_quant_rows<XT, MODE, true>), grid, dim3(256), 0, stream, xp, x_sm, x_sk,
+                       static_cast<int>(M), static_cast<int>(K), q, q_sm, static_cast<int>(k_pad), step);
+  else
+    hipLaunchKernelGGL((k_quant_rows<XT, MODE, false>), grid, dim3(256), 0, stream, xp, x_sm, x_sk,
+                       static_cast<int>(M), static_cast<int>(K), q, q_sm, static_cast<int>(k_pad), step);
+  return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_quant_mode(const void* x, int x_dtype, int64_t x_sm, int64_t x_sk, int64_t M,
+                             int64_t K, int8_t* q, int64_t q_sm, int64_t k_pad, float* step,
+                             hipStream_t stream) {
+  switch (x_dtype) {
+    case QG_F32: return launch_quant_t<QG_F32, MODE>(x, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
+    case QG_F16: return launch_quant_t<QG_F16, MODE>(x, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
+    case QG_BF16: return launch_quant_t<QG_BF16, MODE>(x, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
+    case QG_E4M3: return launch_quant_t<QG_E4M3, MODE>(x, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
+    case QG_E5M2: return launch_quant_t<QG_E5M2, MODE>(x, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_pack_rows_i8(const int8_t* src, int64_t s_r, int64_t s_k,
+                                                      int64_t rows, int64_t K, int8_t* dst,
+                                                      int64_t k_pad) {
+  const int64_t total = rows * k_pad;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = i / k_pad, k = i - r * k_pad;
+    dst[i] = k < K ? src[r * s_r + k * s_k] : static_cast<int8_t>(0);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t x_sm, int64_t x_sk, int64_t M,
+                             int64_t K, int8_t* q, int64_t q_sm, int64_t k_pad, float* step,
+                             int rounding, hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  if (rounding == QG_ROUND_HALF_EVEN)
+    return launch_quant_mode<QG_ROUND_HALF_EVEN>(x, x_dtype, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
+  return launch_quant_mode<QG_ROUND_HALF_AWAY>(x, x_dtype, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
+}
+
+hipError_t launch_pack_rows_i8(const int8_t* src, int64_t s_r, int64_t s_k, int64_t rows, int64_t K,
+                               int8_t* dst, int64_t k_pad, hipStream_t stream) {
+  const int64_t total = rows * k_pad;
+  if (total == 0) return hipSuccess;
+  const int64_t blocks = ceil_div<int64_t>(total, 256);
+  const unsigned grid = static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
+  hipLaunchKernelGGL(k_pack_rows_i8, dim3(grid), dim3(256), 0, stream, src, s_r, s_k, rows, K, dst, k_pad);
+  return hipGetLastError();
+}
+
+}  // namespace qg

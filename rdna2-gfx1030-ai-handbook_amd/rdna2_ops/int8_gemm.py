@@ -1,0 +1,340 @@
+# SPDX-License-Identifier: Apache-2.0
+"""gfx950 INT8 GEMM with an optional FP32 dequantization epilogue (MI355X).
+
+Drop-in for rdna2-ops/rdna2_ops/int8_gemm.py: the same entry points, argument
+meaning, validation order and exceptions, served by hand-written gfx950 HIP
+kernels in librdna2_qgemm.so (int8 MFMA, LDS-DMA pipeline) instead of Triton.
+
+The two scale products retain their order: float(acc) * (row_scale * col_scale).
+rounding="separate" keeps multiply and add separate (MOSS eager semantics,
+int8_gemm.py:53-63 with enable_fp_fusion=False); rounding="fused" uses one FMA
+for multiply+bias (int8_gemm.py:191, the patientx behaviour).
+
+Triton launch knobs (tile, num_warps, num_stages, group_m, wrapped,
+partial_dot) are accepted and validated exactly as the reference does
+(int8_gemm.py:144-147, :155-156) so callers keep working; on MI355X they are
+hints only — the library picks its own MFMA tile — and results never depend
+on them (integer accumulation is exact; the epilogue is per element).
+
+New keyword arguments (defaults keep the reference's behaviour):
+``out_dtype`` (fp32 default; fp16/bf16 round the fp32 epilogue once, RNE),
+``activation`` (None or "gelu_tanh", applied in fp32 before rounding) and
+``epilogue_order`` ("reference" = order above, "eager" = Kitchen's eager
+order, comfy_int8.py:128-143: round(acc*scale) then + round(bias) in out dtype).
+"""
+from contextlib import contextmanager
+import sys
+
+import torch
+
+from . import _lib
+
+_MAX_K = 131071
+
+
+def _validate(a, b, tile, num_warps, num_stages, group_m):
+    """Contract of rdna2-ops/rdna2_ops/int8_gemm.py:131-149 (arch: gfx950)."""
+    if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError("Expected [M,K] @ [K,N]")
+    if a.dtype != torch.int8 or b.dtype != torch.int8:
+        raise TypeError("Both GEMM operands must be INT8")
+    if a.device.type != "cuda" or b.device != a.device:
+        raise ValueError("Inputs must share a HIP device")
+    _lib.require_gfx950(a)
+    if any(s < 0 for s in a.stride() + b.stride()):
+        raise ValueError("Negative strides are unsupported")
+    if a.shape[1] > _MAX_K:
+        raise ValueError("K could overflow signed INT32 for arbitrary signed INT8 inputs")
+    if len(tile) != 3 or any(v < 16 or v > 256 or v & (v - 1) for v in tile):
+        raise ValueError("Tile dimensions must be powers of two in [16,256]")
+    if num_warps not in (4, 8) or num_stages not in (1, 2, 3) or group_m not in (1, 2, 4, 8):
+        raise ValueError("Unsupported launch configuration")
+    if torch.compiler.is_compiling() or torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("Only explicit eager calls are supported")
+
+
+_OUT_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+_ACTIVATIONS = {None: 0, "gelu_tanh": _lib.EPI_GELU_TANH}
+
+
+def _epilogue_flags(rounding, activation, epilogue_order):
+    if activation not in _ACTIVATIONS:
+        raise ValueError("activation must be None or 'gelu_tanh'")
+    if epilogue_order not in ("reference", "eager"):
+        raise ValueError("epilogue_order must be 'reference' or 'eager'")
+    flags = _ACTIVATIONS[activation]
+    if epilogue_order == "eager":
+        if activation is not None or rounding == "fused":
+            raise ValueError("The eager epilogue order has no activation and no FMA rounding")
+        flags |= _lib.EPI_ORDER_EAGER
+    elif rounding == "fused":
+        flags |= _lib.EPI_ORDER_FUSED_FMA
+    return flags
+
+
+def _launch(a, b, a_scale, b_scale, bias, *, tile, num_warps, num_stages, group_m, rounding,
+            return_kernel, wrapped=False, partial_dot=False, out_dtype=torch.float32,
+            activation=None, epilogue_order="reference"):
+    """Host dispatch of rdna2-ops/rdna2_ops/int8_gemm.py:152-192 onto the C ABI."""
+    _validate(a, b, tile, num_warps, num_stages, group_m)
+    if partial_dot and not wrapped:
+        raise ValueError("partial_dot requires the explicitly wrapped-load variant")
+    dequant = a_scale is not None
+    m, k = a.shape
+    n = b.shape[1]
+    if rounding not in ("separate", "fused"):
+        raise ValueError("rounding must be separate or fused")
+    if dequant:
+        for value, size, label in ((a_scale, m, "a_scale"), (b_scale, n, "b_scale")):
+            if not isinstance(value, torch.Tensor):
+                raise TypeError(label + " must be a device tensor")
+            if value.device != a.device or value.dtype != torch.float32 or not value.is_contiguous():
+                raise ValueError(label + " must be contiguous FP32 on the input device")
+            if value.numel() != size and not (label == "b_scale" and value.numel() == 1):
+                raise ValueError(label + " has the wrong number of elements")
+            if torch.is_grad_enabled() and value.requires_grad:
+                raise ValueError("Autograd is unsupported")
+        if bias is not None:
+            if (bias.device != a.device or bias.numel() != n or not bias.is_contiguous()
+                    or bias.dtype not in (torch.float32, torch.float16, torch.bfloat16)):
+                raise ValueError("Bias must be a contiguous floating point vector of length N")
+            if torch.is_grad_enabled() and bias.requires_grad:
+                raise ValueError("Autograd is unsupported")
+        if out_dtype not in _OUT_DTYPES:
+            raise ValueError("out_dtype must be float32, float16 or bfloat16")
+        flags = _epilogue_flags(rounding, activation, epilogue_order)
+    else:
+        if out_dtype not in (torch.float32, torch.int32) or activation is not None:
+            raise ValueError("The integer GEMM has no dtype conversion or activation")
+        flags = 0
+    odt = out_dtype if dequant else torch.int32
+    out = torch.empty((m, n), device=a.device, dtype=odt)
+    if m == 0 or n == 0:
+        return (out, None) if return_kernel else out
+    lib = _lib.library()
+    ws_bytes = lib.qg_int8_gemm_workspace_bytes(
+        _lib.ptr(a), a.stride(0), a.stride(1), _lib.ptr(b), b.stride(0), b.stride(1), m, n, k)
+    ws = _lib.workspace(ws_bytes, a.device)
+    wsp, wsn = _lib.ws_ptr(ws)
+    status = lib.qg_int8_gemm(
+        _lib.ptr(a), a.stride(0), a.stride(1), _lib.ptr(b), b.stride(0), b.stride(1), m, n, k,
+        _lib.ptr(a_scale) if dequant else None, _lib.ptr(b_scale) if dequant else None,
+        b_scale.numel() if dequant else 0,
+        _lib.ptr(bias) if dequant else None,
+        _lib.DTYPE_CODE[bias.dtype] if (dequant and bias is not None) else 0,
+        _lib.ptr(out), _lib.DTYPE_CODE[odt], flags, wsp, wsn, _lib.stream_of(a))
+    _lib.check(status, "qg_int8_gemm")
+    if not return_kernel:
+        return out
+    big = (-(-m // 256)) * (-(-n // 192)) >= 192
+    tile_used = (256, 192, 64) if big else (128, 128, 64)
+    meta = _lib.kernel_metadata("int8_mfma_16x16x64_lds_dma", tile_used,
+                                "k_i8_gemmILi256ELi192E" if big else "k_i8_gemmILi128ELi128E")
+    meta.update(packed_operands=ws_bytes > 0, requested_tile=list(tile), epilogue_flags=flags)
+    return out, meta
+
+
+def int8_matmul(a, b, *, tile=(32, 64, 64), num_warps=4, num_stages=1,
+                group_m=4, return_kernel=False, wrapped=False, partial_dot=False):
+    """Exact INT8 -> INT32 matmul; accepts both [K,N] layouts without copying.
+
+    Mirrors rdna2-ops/rdna2_ops/int8_gemm.py:195-200. ``b`` may be ``weight.T``
+    (strides (1, K), read in place) or any other positive-stride [K, N] view
+    (packed once into workspace by the library).
+    """
+    return _launch(a, b, None, None, None, tile=tile, num_warps=num_warps,
+                   num_stages=num_stages, group_m=group_m, rounding="separate",
+                   return_kernel=return_kernel, wrapped=wrapped, partial_dot=partial_dot)
+
+
+def int8_gemm_dequant(a, b, a_scale, b_scale, bias=None, *, tile=(32, 64, 64),
+                      num_warps=4, num_stages=1, group_m=4,
+                      rounding="separate", return_kernel=False, wrapped=False, partial_dot=False,
+                      out_dtype=torch.float32, activation=None, epilogue_order="reference"):
+    """INT32 GEMM and row/scalar or row/column FP32 dequantization in one kernel.
+
+    Mirrors rdna2-ops/rdna2_ops/int8_gemm.py:203-214. Inputs are already
+    quantized. A fresh contiguous output is allocated. Finite scales/bias are a
+    precondition; no GPU-wide finite scan is inserted.
+    """
+    return _launch(a, b, a_scale, b_scale, bias, tile=tile, num_warps=num_warps,
+                   num_stages=num_stages, group_m=group_m, rounding=rounding,
+                   return_kernel=return_kernel, wrapped=wrapped, partial_dot=partial_dot,
+                   out_dtype=out_dtype, activation=activation, epilogue_order=epilogue_order)
+
+
+def w8a8_linear(x, weight, weight_scale, bias=None, *, out_dtype=None, activation=None,
+                rounding="half_even", epilogue_order="reference"):
+    """Fused W8A8 linear: per-token INT8 quantization of ``x`` (absmax/127),
+    INT8 MFMA GEMM against ``weight`` [N, K] and the dequant/bias/activation
+    epilogue, in one library call (qg_w8a8_linear).
+
+    x: [..., K] fp32/fp16/bf16 with unit K stride. weight: int8 [N, K].
+    weight_scale: fp32 [N] (or [N, 1]) or a one-element tensor.
+    rounding: "half_even" (BASELINE per-token rule) or "half_away" (the
+    reference's in-tree _quant_rows, fp8_weight_gemm_v06.py:87-90).
+    out_dtype defaults to x.dtype.
+    """
+    if x.dtype not in _OUT_DTYPES or weight.dtype != torch.int8 or weight.ndim != 2:
+        raise TypeError("x must be fp32/fp16/bf16 and weight int8 [N, K]")
+    if x.shape[-1] != weight.shape[1]:
+        raise ValueError("Input and weight inner dimensions differ")
+    if x.device.type != "cuda" or weight.device != x.device:
+        raise ValueError("Inputs must share a HIP device")
+    _lib.require_gfx950(x)
+    if rounding not in ("half_even", "half_away"):
+        raise ValueError("rounding must be half_even or half_away")
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out_dtype not in _OUT_DTYPES:
+        raise ValueError("out_dtype must be float32, float16 or bfloat16")
+    k = x.shape[-1]
+    if k > _MAX_K:
+        raise ValueError("K could overflow signed INT32 for arbitrary signed INT8 inputs")
+    n = weight.shape[0]
+    ws_scale = weight_scale.reshape(-1)
+    if (ws_scale.dtype != torch.float32 or ws_scale.device != x.device or not ws_scale.is_contiguous()
+            or ws_scale.numel() not in (1, n)):
+        raise ValueError("weight_scale must be contiguous FP32 with 1 or N elements")
+    if bias is not None and (bias.device != x.device or bias.numel() != n or not bias.is_contiguous()
+                             or bias.dtype not in _OUT_DTYPES):
+        raise ValueError("Bias must be a contiguous floating point vector of length N")
+    if weight.stride(1) != 1:
+        weight = weight.contiguous()
+    x2 = x.reshape(-1, k)
+    if k and x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    flags = _epilogue_flags("separate", activation, epilogue_order)
+    out = torch.empty((m, n), device=x.device, dtype=out_dtype)
+    if m and n:
+        lib = _lib.library()
+        need = lib.qg_w8a8_linear_workspace_bytes(_lib.ptr(weight), weight.stride(0), m, n, k)
+        ws = _lib.workspace(need, x.device)
+        wsp, wsn = _lib.ws_ptr(ws)
+        status = lib.qg_w8a8_linear(
+            _lib.ptr(x2), _lib.DTYPE_CODE[x2.dtype], x2.stride(0), m, k, _lib.ptr(weight),
+            weight.stride(0), n, _lib.ptr(ws_scale), ws_scale.numel(), _lib.ptr(bias),
+            _lib.DTYPE_CODE[bias.dtype] if bias is not None else 0, _lib.ptr(out),
+            _lib.DTYPE_CODE[out_dtype],
+            _lib.ROUND_HALF_EVEN if rounding == "half_even" else _lib.ROUND_HALF_AWAY,
+            flags, wsp, wsn, _lib.stream_of(x))
+        _lib.check(status, "qg_w8a8_linear")
+    return out.reshape(*x.shape[:-1], n)
+
+
+@contextmanager
+def moss_int8_gemm_candidate(*, tile=(32, 64, 64), num_warps=4,
+                             num_stages=1, group_m=4, wrapped=False, partial_dot=False):
+    """Scoped MOSS eager export replacement in an exclusively owned process.
+
+    Mirrors rdna2-ops/rdna2_ops/int8_gemm.py:217-271: preserves Kitchen's input
+    activation, ConvRot, row quantizer and residual helpers; FP32 input/output
+    only; all other calls use the saved exported callable. No registry, code
+    object, source file or model weight is changed.
+    """
+    from comfy_kitchen.backends import eager as backend
+    from comfy_kitchen.backends.eager import quantization as q
+    original = backend.int8_linear
+    stats = {"hits": 0, "fallbacks": 0, "shapes": {}}
+
+    def candidate(x, weight, weight_scale, bias=None, out_dtype=torch.bfloat16,
+                  convrot=False, convrot_groupsize=256, input_act=None,
+                  input_act_weight=None, input_act_eps=0.0,
+                  residual=None, residual_scale=None):
+        if x.dtype != torch.float32 or out_dtype != torch.float32:
+            stats["fallbacks"] += 1
+            return original(x, weight, weight_scale, bias=bias, out_dtype=out_dtype,
+                            convrot=convrot, convrot_groupsize=convrot_groupsize,
+                            input_act=input_act, input_act_weight=input_act_weight,
+                            input_act_eps=input_act_eps, residual=residual,
+                            residual_scale=residual_scale)
+        x = q._apply_input_act(x, input_act, input_act_weight, input_act_eps)
+        if x.shape[-1] != weight.shape[-1]:
+            raise ValueError("Input and weight inner dimensions differ")
+        weight = weight.to(device=x.device).contiguous()
+        ws = weight_scale.to(device=x.device, dtype=torch.float32).reshape(-1)
+        if ws.numel() not in (1, weight.shape[0]):
+            raise ValueError("Weight scale must be scalar or per output channel")
+        if convrot:
+            if x.shape[-1] % convrot_groupsize:
+                raise ValueError("ConvRot group size does not divide K")
+            h = q._build_hadamard(convrot_groupsize, device=x.device, dtype=x.dtype)
+            x = q._rotate_activation(x, h, convrot_groupsize)
+        shape = x.shape
+        a, sa = q.quantize_int8_rowwise(x.reshape(-1, shape[-1]))
+        bias32 = None if bias is None else bias.to(device=x.device, dtype=torch.float32).reshape(-1)
+        y = int8_gemm_dequant(a, weight.T, sa, ws, bias32, tile=tile,
+                              num_warps=num_warps, num_stages=num_stages,
+                              group_m=group_m, rounding="separate", wrapped=wrapped,
+                              partial_dot=partial_dot)
+        stats["hits"] += 1
+        key = str((a.shape[0], weight.shape[0], a.shape[1]))
+        stats["shapes"][key] = stats["shapes"].get(key, 0) + 1
+        return q._apply_residual(y.reshape(*shape[:-1], weight.shape[0]), residual, residual_scale)
+
+    backend.int8_linear = candidate
+    try:
+        yield stats
+    finally:
+        if backend.int8_linear is not candidate:
+            raise RuntimeError("MOSS eager export changed during the research context")
+        backend.int8_linear = original
+
+
+@contextmanager
+def qwen_int8_gemm_candidate(patch_module=None, *, tile=(32, 64, 64),
+                             num_warps=4, num_stages=1, group_m=4, wrapped=False, partial_dot=False):
+    """Scoped replacement of the patientx bridge's two GEMM wrappers.
+
+    Mirrors rdna2-ops/rdna2_ops/int8_gemm.py:274-330. The original patientx row
+    quantizer stays in use; the epilogue uses FMA rounding like patientx.
+    """
+    if patch_module is None:
+        found = [mod for mod in tuple(sys.modules.values()) if mod is not None
+                 and str(getattr(mod, "__file__", "")).endswith(
+                     "RDNA2-Qwen21-INT8/rocm_int8_kitchen_patch.py")]
+        if len(found) != 1:
+            raise RuntimeError("Expected one already-loaded Qwen patientx bridge")
+        patch_module = found[0]
+    originals = {name: getattr(patch_module, name) for name in
+                 ("triton_int8_linear", "triton_int8_linear_per_row")}
+    stats = {"hits": 0, "fallbacks": 0, "shapes": {}}
+    replacements = {}
+
+    def make_wrapper(original, per_row):
+        quantize = original.__globals__["triton_quantize_rowwise"]
+
+        def candidate(x, weight, weight_scale, bias=None, compute_dtype=torch.float16):
+            if x.dtype != torch.float32 or compute_dtype != torch.float32:
+                stats["fallbacks"] += 1
+                return original(x, weight, weight_scale, bias=bias, compute_dtype=compute_dtype)
+            shape = x.shape
+            x2d = x.reshape(-1, shape[-1])
+            a, sa = quantize(x2d.float() if per_row else x2d)
+            if per_row:
+                ws = weight_scale.reshape(weight.shape[0]).contiguous()
+            elif isinstance(weight_scale, torch.Tensor):
+                ws = weight_scale.to(x.device, non_blocking=True).reshape(-1)
+            else:
+                ws = torch.tensor([weight_scale], device=x.device, dtype=torch.float32)
+            y = int8_gemm_dequant(a, weight.T, sa, ws, bias, tile=tile,
+                                  num_warps=num_warps, num_stages=num_stages,
+                                  group_m=group_m, rounding="fused", wrapped=wrapped,
+                                  partial_dot=partial_dot)
+            stats["hits"] += 1
+            key = str((a.shape[0], weight.shape[0], a.shape[1]))
+            stats["shapes"][key] = stats["shapes"].get(key, 0) + 1
+            return y.reshape(*shape[:-1], weight.shape[0])
+        return candidate
+
+    for name, original in originals.items():
+        replacements[name] = make_wrapper(original, name.endswith("per_row"))
+        setattr(patch_module, name, replacements[name])
+    try:
+        yield stats
+    finally:
+        for name in originals:
+            if getattr(patch_module, name) is not replacements[name]:
+                raise RuntimeError("Qwen patientx callable changed during the research context")
+        for name, original in originals.items():
+            setattr(patch_module, name, original)

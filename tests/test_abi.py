@@ -1,0 +1,87 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/qgemm.h declares with the argument count the ctypes binding uses, and
+rejects invalid arguments with hipErrorInvalidValue before any HIP call
+(the convention of rdna2-ops/rdna2_ops/csrc/group_norm_silu.hip:298-317)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from rdna2_ops import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "qgemm.h"
+INVALID = 1  # hipErrorInvalidValue
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(qg_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.M | re.S):
+        args = m.group(2).strip()
+        decls[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.library()
+
+
+def test_header_declares_bound_functions():
+    decls = declared_functions()
+    assert set(decls) == set(_lib.SIGNATURES), set(decls) ^ set(_lib.SIGNATURES)
+    for name, nargs in decls.items():
+        assert nargs == len(_lib.SIGNATURES[name][1]), name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+    assert lib.qg_version().decode().startswith("librdna2_qgemm gfx950")
+
+
+def test_error_string(lib):
+    assert lib.qg_error_string(0)
+    assert lib.qg_error_string(INVALID)
+
+
+def test_int8_gemm_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    base = dict(a=p, a_sm=64, a_sk=1, b=p, b_sk=1, b_sn=64, m=4, n=4, k=64, a_scale=p, b_scale=p,
+                b_scale_numel=4, bias=None, bias_dtype=0, out=p, out_dtype=0, epilogue=0,
+                workspace=None, workspace_bytes=0, stream=None)
+
+    def call(**kw):
+        args = dict(base, **kw)
+        return lib.qg_int8_gemm(*args.values())
+
+    assert call(m=-1) == INVALID
+    assert call(k=131072) == INVALID                       # int8_gemm.py:142-143
+    assert call(a_sm=-64) == INVALID                       # negative strides (:140-141)
+    assert call(b_scale_numel=3) == INVALID                # wrong scale length (:168)
+    assert call(out_dtype=_lib.I32) == INVALID             # dequant needs a float output
+    assert call(a_scale=None, b_scale=None, out_dtype=_lib.F32) == INVALID  # int GEMM -> int32
+    assert call(bias=p, bias_dtype=_lib.I8) == INVALID     # bias dtype (:173-175)
+    assert call(epilogue=_lib.EPI_ORDER_EAGER | _lib.EPI_GELU_TANH) == INVALID
+    assert call(epilogue=64) == INVALID
+    assert call(a_sk=2) == INVALID                         # needs packing -> workspace missing
+    assert call(m=0) == 0 and call(n=0, b_scale_numel=1) == 0  # empty output: nothing to launch
+
+
+def test_quant_rows_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(16)
+    assert lib.qg_quant_rows_i8(p, _lib.I8, 8, 1, 2, 8, p, 8, p, 0, None) == INVALID
+    assert lib.qg_quant_rows_i8(p, _lib.F16, 8, 1, 2, 8, p, 8, p, 7, None) == INVALID
+    assert lib.qg_quant_rows_i8(p, _lib.F16, 8, 1, 2, 8, p, 4, p, 0, None) == INVALID  # q_sm < k
+    assert lib.qg_quant_rows_i8(p, _lib.F16, 8, 1, 0, 8, p, 8, p, 0, None) == 0
+
+
+def test_w8a8_linear_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(16)
+    args = [p, _lib.F16, 64, 4, 64, p, 64, 4, p, 4, None, 0, p, _lib.F16, 0, 0, None, 0, None]
+    assert lib.qg_w8a8_linear(*args) == INVALID            # workspace missing
+    bad = list(args)
+    bad[1] = _lib.I8
+    assert lib.qg_w8a8_linear(*bad) == INVALID
+    assert lib.qg_w8a8_linear_workspace_bytes(p, 64, 4, 4, 64) >= 4 * 64 + 16

@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--cpu-rows", type=int, default=128, help="tokens in the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 512 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -154,6 +156,16 @@ def main():
     from rdna2_ops.quantize import quantize_int8_rowwise
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        # A plain copy of known size: 512 MiB read + 512 MiB written per launch
+        # (larger than the 256 MB Infinity Cache), for scaling HBM counters.
+        src = torch.ones(512 * 2 ** 20 // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_each_way": src.numel() * 4, "launches": 5}), flush=True)
+        return
     lib = _lib.library()
     chain = Chain(torch, lib, _lib, quantize_int8_rowwise, synthetic.cfg1(), dev)
     for _ in range(args.warmup):

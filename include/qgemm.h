@@ -101,9 +101,10 @@ int qg_quant_rows_i8(const void* x, int x_dtype, int64_t x_sm, int64_t x_sk,
  * Otherwise a_scale: [m] fp32, b_scale: [n] fp32 (b_scale_numel == n) or a
  * scalar (b_scale_numel == 1); bias: NULL or [n] of bias_dtype
  * (QG_F32/QG_F16/QG_BF16); out_dtype QG_F32 / QG_F16 / QG_BF16.
- * out: [m, n] contiguous. Non-canonical strides or k % 64 != 0 are packed into
+ * out: [m, n] contiguous. Non-canonical strides or k % 128 != 0 are packed into
  * the workspace first (see qg_int8_gemm_workspace_bytes).
- * k must be <= 131071 (int8_gemm.py:142-143).
+ * k must be <= 131071 (int8_gemm.py:142-143); each (packed) operand must be
+ * smaller than 2 GiB.
  * ------------------------------------------------------------------------- */
 size_t qg_int8_gemm_workspace_bytes(const void* a, int64_t a_sm, int64_t a_sk,
                                     const void* b, int64_t b_sk, int64_t b_sn,
@@ -123,9 +124,9 @@ int qg_int8_gemm(const int8_t* a, int64_t a_sm, int64_t a_sk, const int8_t* b,
  *   (fp8_weight_gemm_v06.py:181-193).
  * x: [m, k] (x_dtype QG_F32/QG_F16/QG_BF16, row stride x_sm, unit k stride);
  * w: [n, k] int8 row-major (row stride w_sn); w_scale [n] or scalar.
- * The workspace holds the int8 activations ([m, round_up(k, 64)]), their fp32
+ * The workspace holds the int8 activations ([m, round_up(k, 128)]), their fp32
  * steps ([m]) and, when w is not canonical ([n, k] with unit k stride,
- * 16-byte aligned rows and k % 64 == 0), a zero-padded packed copy of w; its
+ * 16-byte aligned rows and k % 128 == 0), a zero-padded packed copy of w; its
  * size comes from qg_w8a8_linear_workspace_bytes.
  * ------------------------------------------------------------------------- */
 size_t qg_w8a8_linear_workspace_bytes(const int8_t* w, int64_t w_sn, int64_t m,

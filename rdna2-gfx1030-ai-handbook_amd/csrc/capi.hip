@@ -18,10 +18,16 @@ constexpr int64_t kIntMax = 2147483647;
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// A [m, k] (strides a_sm, a_sk) can be read in place by the GEMM kernel.
+// The GEMM kernel streams K in 128-byte stages and addresses an operand with
+// 32-bit byte offsets from its base.
+constexpr int64_t kStageK = 128;
+constexpr int64_t kMaxOperandBytes = int64_t(1) << 31;
+
+// An operand of `rows` rows (row stride s_row, element stride s_k) can be read
+// in place by the GEMM kernel.
 inline bool canonical_rows(const void* p, int64_t s_row, int64_t s_k, int64_t rows, int64_t k) {
-  (void)rows;
-  return s_k == 1 && (s_row % 16) == 0 && aligned16(p) && (k % 64) == 0;
+  return s_k == 1 && (s_row % 16) == 0 && aligned16(p) && (k % kStageK) == 0 &&
+         (rows - 1) * s_row + k < kMaxOperandBytes;
 }
 
 inline bool float_dtype(int d) { return d == QG_F32 || d == QG_F16 || d == QG_BF16; }
@@ -36,7 +42,7 @@ struct I8Plan {
 I8Plan plan_i8(const void* a, int64_t a_sm, int64_t a_sk, const void* b, int64_t b_sk,
                int64_t b_sn, int64_t m, int64_t n, int64_t k) {
   I8Plan pl;
-  pl.kp = round_up(k, 64);
+  pl.kp = round_up(k, kStageK);
   // B = W^T: W [n, k] has row stride b_sn and element stride b_sk.
   pl.pack_a = !canonical_rows(a, a_sm, a_sk, m, k);
   pl.pack_b = !canonical_rows(b, b_sn, b_sk, n, k);
@@ -109,6 +115,7 @@ int int8_gemm_impl(const int8_t* a, int64_t a_sm, int64_t a_sk, const int8_t* b,
   const I8Plan pl = plan_i8(a, a_sm, a_sk, b, b_sk, b_sn, m, n, k);
   if (pl.total() > 0 && (!workspace || workspace_bytes < pl.total() || !aligned16(workspace)))
     return hipErrorInvalidValue;
+  if (m * pl.kp >= kMaxOperandBytes || n * pl.kp >= kMaxOperandBytes) return hipErrorInvalidValue;
 
   qg::I8GemmArgs p{};
   p.M = static_cast<int>(m);
@@ -170,7 +177,7 @@ struct W8A8Plan {
 };
 W8A8Plan plan_w8a8(const void* w, int64_t w_sn, int64_t m, int64_t n, int64_t k) {
   W8A8Plan pl;
-  pl.kp = round_up(k, 64);
+  pl.kp = round_up(k, kStageK);
   pl.act_bytes = static_cast<size_t>(round_up(m * pl.kp, 256));
   pl.step_bytes = static_cast<size_t>(round_up(m * 4, 256));
   pl.w = plan_i8(nullptr, pl.kp, 1, w, 1, w_sn, m, n, k);
@@ -201,6 +208,7 @@ extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t 
   if (!out || (k > 0 && (!x || !w))) return hipErrorInvalidValue;
   const W8A8Plan pl = plan_w8a8(w, w_sn, m, n, k);
   if (!workspace || workspace_bytes < pl.total() || !aligned16(workspace)) return hipErrorInvalidValue;
+  if (m * pl.kp >= kMaxOperandBytes || n * pl.kp >= kMaxOperandBytes) return hipErrorInvalidValue;
   char* ws = static_cast<char*>(workspace);
   int8_t* xq = reinterpret_cast<int8_t*>(ws);
   float* xs = reinterpret_cast<float*>(ws + pl.act_bytes);

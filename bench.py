@@ -41,7 +41,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-rows", type=int, default=128, help="tokens in the CPU-baseline sample")
+    ap.add_argument("--cpu-rows", type=int, default=4096, help="tokens in the CPU-baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -144,6 +145,17 @@ def run_cfg0(torch, lib, _lib, quantize, synthetic, dev, iters=50):
             "cfg0_w8a8_linear_tops": round(lin_tops, 1)}
 
 
+def traffic_bytes():
+    """HBM bytes per launch of the GEMM kernel in this chain, measured with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a plain-copy calibration)
+    and recorded in profiles/int8_gemm_cfg1_chain_traffic.json; None if absent."""
+    path = ROOT / "profiles" / "int8_gemm_cfg1_chain_traffic.json"
+    try:
+        return json.loads(path.read_text())["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -208,7 +220,7 @@ def main():
                                "per-token int8 quant prologue on each GEMM; fp16 in/out",
                    "tokens": chain.m, "hidden": 3072, "ops_per_step": ops},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS,
-                     "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_bytes(),
                      "kernel": "k_i8_gemm<256,192> (int8 MFMA GEMM + fused epilogue)",
                      "per_launch": layer_info},
     }
@@ -216,7 +228,7 @@ def main():
         line["secondary"] = run_cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev)
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import time_cfg1_chain
-        cpu_ops, cpu_s, threads, sample = time_cfg1_chain(rows=args.cpu_rows)
+        cpu_ops, cpu_s, threads, sample = time_cfg1_chain(rows=args.cpu_rows, seconds=args.cpu_seconds)
         line["cpu_baseline"] = {"value": round(cpu_ops / 1e12, 4), "unit": "TOPS", "cores": threads,
                                 "kind": "port", "sample": sample, "seconds_per_sample": round(cpu_s, 3)}
     print(json.dumps(line), flush=True)

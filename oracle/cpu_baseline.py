@@ -33,10 +33,11 @@ def w8a8_linear_cpu(x, wq_t, ws, bias, activation=None):
     return v.to(torch.float16)
 
 
-def time_cfg1_chain(rows=128, hidden=3072, threads=None, repeats=3, seed=1):
-    """Time the cfg1 chain (QKV, up+GELU, down) on ``rows`` tokens on the CPU.
+def time_cfg1_chain(rows=4096, hidden=3072, threads=None, seconds=10.0, seed=1):
+    """Time the cfg1 chain (QKV, up+GELU, down) on ``rows`` tokens on the CPU,
+    repeating whole passes for about ``seconds`` (at least two).
 
-    Returns (ops_per_second, seconds_per_pass, threads, sample description).
+    Returns (ops_per_second, median_seconds_per_pass, threads, sample description).
     The weights are random int8 of the real shapes (their values do not change
     the CPU work); the activations are the first ``rows`` tokens' worth of a
     seeded N(0,1) input.
@@ -60,11 +61,13 @@ def time_cfg1_chain(rows=128, hidden=3072, threads=None, repeats=3, seed=1):
 
     one_pass()  # warm-up
     times = []
-    for _ in range(repeats):
+    start = time.perf_counter()
+    while len(times) < 2 or time.perf_counter() - start < seconds:
         t0 = time.perf_counter()
         one_pass()
         times.append(time.perf_counter() - t0)
     times.sort()
     sec = times[len(times) // 2]
     ops = 2 * rows * hidden * (3 * hidden + 4 * hidden + 4 * hidden)
-    return ops / sec, sec, threads, f"cfg1 chain on {rows} of 4096 tokens (torch CPU, median of {repeats})"
+    return ops / sec, sec, threads, (f"cfg1 chain on {rows} of 4096 tokens, torch CPU int8 (_int_mm), "
+                                     f"median of {len(times)} passes in {time.perf_counter() - start:.1f} s")

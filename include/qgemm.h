@@ -65,7 +65,8 @@ enum qg_w4_flags {
   QG_W4_ORDER_HIGH = 2,     /* nibble i of a word at bits 28-4i (order="high") */
   QG_W4_LAYOUT_KN = 4,      /* words are [K/8, N] (layout="kn") instead of [N, K/8] */
   QG_W4_ZEROS_PACKED = 8    /* zero points are uint4 packed 8 per int32 along the
-                               group axis, [N, ceil(G/8)]; else int32 [N, G] */
+                               group axis, [N, ceil((K/G)/8)], group g at bits
+                               4*(g%8) of word g/8; else int32 [N, K/G] */
 };
 
 /* Error string of a returned status. Mirrors rdna2_hip_error_string
@@ -137,6 +138,71 @@ int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t m,
                    const void* bias, int bias_dtype, void* out, int out_dtype,
                    int rounding, int epilogue, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * INT4 weight storage (W4).
+ * A W4 weight [n, k] quantised in groups of G = group_size (32, 64 or 128)
+ * consecutive K values per output row n:
+ *   data   int32 words, 8 nibbles each: [n, k/8] ("nk") or [k/8, n]
+ *          (QG_W4_LAYOUT_KN); nibble e of a word holds K index 8*word + e at
+ *          bits 4e, or 28-4e with QG_W4_ORDER_HIGH;
+ *   scales [n, k/G] fp32 or bf16;
+ *   zeros  [n, k/G] int32, or uint4 packed (QG_W4_ZEROS_PACKED);
+ *   weight = (q - zero) * scale.
+ * QG_W4_SIGNED_NIBBLES selects the reference PackedInt4 coordinates
+ * (int4_weight_gemm_v07.py:20-82): q in [-8, 7] stored as q & 15, zero points
+ * in the same signed coordinates. Without it nibbles and zero points are
+ * unsigned uint4 (flags = QG_W4_ZEROS_PACKED,
+ * bf16 scales, G = 128).
+ * Shape contract (int4_weight_gemm_v07.py:436-440): n, k > 0, k % G == 0,
+ * n * k < 2^31.
+ * ------------------------------------------------------------------------- */
+
+/* Quantise and pack a floating [n, k] weight (strides w_sn, w_sk > 0; w_dtype
+ * QG_F32/QG_F16/QG_BF16).
+ * Replaces: pack_int4 / _pack_weight (int4_weight_gemm_v07.py:103-133, :413-430),
+ *   which must equal pack_int4_cpu (:49-82).
+ * Per group, fp32 IEEE division and round-half-to-even throughout:
+ *   symmetric:  s = absmax / 7, q = clamp(round(x / s), -7, 7), zero = 0;
+ *   asymmetric: lo = min(min x, 0), hi = max(max x, 0), s = (hi - lo) / 15,
+ *               zu = clamp(round(-lo / s), 0, 15),
+ *               q = clamp(round(x / s) + zu, 0, 15) (unsigned coordinates);
+ * s is rounded to scales_dtype before it is used; a group whose s is 0 gets
+ * s = 1 (and, in signed coordinates, q = zero = 0, :74-75).
+ * sums: NULL or [n, k/G] int32, the per-group sum of the stored codes. */
+int qg_w4_pack(const void* w, int w_dtype, int64_t w_sn, int64_t w_sk, int64_t n,
+               int64_t k, int group_size, int symmetric, int flags, int32_t* data,
+               void* scales, int scales_dtype, void* zeros, int32_t* sums,
+               void* stream);
+
+/* Decode a W4 weight to out [n, k] contiguous: (q - zero) * scale rounded once
+ * to out_dtype (QG_F16 / QG_F32 / QG_BF16), or the centred integers q - zero
+ * (QG_I8).
+ * Replaces: unpack_int4 / _unpack_weight (int4_weight_gemm_v07.py:136-151,
+ *   :450-458). */
+int qg_w4_unpack(const int32_t* data, int64_t n, int64_t k, int group_size,
+                 int flags, const void* scales, int scales_dtype,
+                 const void* zeros, void* out, int out_dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * W4A16 linear: out[m, n] = sum_k a[m, k] * ((q[n,k] - zero[n,g]) * scale[n,g])
+ * (+ bias[n]), fp32 accumulation, one rounding to out_dtype.
+ * Replaces: int4_linear_a16 (int4_weight_gemm_v07.py:540-564) with its
+ *   _linear_dot2 kernel (:365-387); the reference rounds every dequantised
+ *   weight to fp16 first, this library applies each group scale to the exact
+ *   group partial sum instead (closer to the exact product).
+ * a: [m, k] QG_F16 or QG_BF16, unit K stride, row stride a_sm (a multiple of 8
+ * elements, 16-byte aligned base); w: 16-byte aligned; out: [m, n] contiguous
+ * QG_F16 / QG_BF16 / QG_F32; bias NULL or [n] of bias_dtype; m * n < 2^31.
+ * The workspace is currently unused (qg_w4a16_gemm_workspace_bytes returns 0);
+ * it is part of the signature so that split-K variants keep the ABI. */
+size_t qg_w4a16_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int group_size,
+                                     int flags);
+int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m, int64_t k,
+                  const int32_t* w, int64_t n, int group_size, int flags,
+                  const void* scales, int scales_dtype, const void* zeros,
+                  const void* bias, int bias_dtype, void* out, int out_dtype,
+                  void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

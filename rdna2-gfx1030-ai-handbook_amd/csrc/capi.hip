@@ -241,3 +241,113 @@ extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t 
   p.epi = epilogue;
   return qg::launch_i8_gemm(p, s);
 }
+
+// --------------------------------------------------------------------------
+// W4 (INT4 weight) storage and the W4A16 GEMM.
+namespace {
+
+constexpr int kW4Flags = QG_W4_SIGNED_NIBBLES | QG_W4_ORDER_HIGH | QG_W4_LAYOUT_KN | QG_W4_ZEROS_PACKED;
+
+// int4_weight_gemm_v07.py:436-440: group 32/64/128 dividing K, nonempty, N*K < 2^31.
+bool valid_w4_shape(int64_t n, int64_t k, int group, int flags) {
+  if (group != 32 && group != 64 && group != 128) return false;
+  if (n <= 0 || k <= 0 || k % group != 0 || n * k >= (int64_t(1) << 31)) return false;
+  return (flags & ~kW4Flags) == 0;
+}
+
+}  // namespace
+
+extern "C" int qg_w4_pack(const void* w, int w_dtype, int64_t w_sn, int64_t w_sk, int64_t n,
+                          int64_t k, int group_size, int symmetric, int flags, int32_t* data,
+                          void* scales, int scales_dtype, void* zeros, int32_t* sums, void* stream) {
+  if (!valid_w4_shape(n, k, group_size, flags)) return hipErrorInvalidValue;
+  if (!float_dtype(w_dtype) || (scales_dtype != QG_F32 && scales_dtype != QG_BF16)) return hipErrorInvalidValue;
+  if (w_sn <= 0 || w_sk <= 0 || symmetric < 0 || symmetric > 1) return hipErrorInvalidValue;
+  if ((n - 1) * w_sn + (k - 1) * w_sk >= (int64_t(1) << 40)) return hipErrorInvalidValue;
+  if (!w || !data || !scales || !zeros) return hipErrorInvalidValue;
+  qg::W4PackArgs p{};
+  p.w = w;
+  p.w_dtype = w_dtype;
+  p.w_sn = w_sn;
+  p.w_sk = w_sk;
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(k);
+  p.group = group_size;
+  p.symmetric = symmetric;
+  p.flags = flags;
+  p.data = data;
+  p.scales = scales;
+  p.scale_dtype = scales_dtype;
+  p.zeros = zeros;
+  p.sums = sums;
+  return qg::launch_w4_pack(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qg_w4_unpack(const int32_t* data, int64_t n, int64_t k, int group_size, int flags,
+                            const void* scales, int scales_dtype, const void* zeros, void* out,
+                            int out_dtype, void* stream) {
+  if (!valid_w4_shape(n, k, group_size, flags)) return hipErrorInvalidValue;
+  if (scales_dtype != QG_F32 && scales_dtype != QG_BF16) return hipErrorInvalidValue;
+  if (!(float_dtype(out_dtype) || out_dtype == QG_I8)) return hipErrorInvalidValue;
+  if (!data || !scales || !zeros || !out) return hipErrorInvalidValue;
+  qg::W4Args p{};
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(k);
+  p.w = reinterpret_cast<const uint32_t*>(data);
+  p.flags = flags;
+  p.group = group_size;
+  p.scales = scales;
+  p.scale_f32 = scales_dtype == QG_F32;
+  p.zeros = zeros;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  return qg::launch_w4_unpack(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t qg_w4a16_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int group_size,
+                                                int flags) {
+  (void)m;
+  (void)n;
+  (void)k;
+  (void)group_size;
+  (void)flags;
+  return 0;
+}
+
+extern "C" int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m, int64_t k,
+                             const int32_t* w, int64_t n, int group_size, int flags,
+                             const void* scales, int scales_dtype, const void* zeros,
+                             const void* bias, int bias_dtype, void* out, int out_dtype,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (!valid_w4_shape(n, k, group_size, flags)) return hipErrorInvalidValue;
+  if (m < 0 || m > kIntMax || m * n >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  if (a_dtype != QG_F16 && a_dtype != QG_BF16) return hipErrorInvalidValue;
+  if (scales_dtype != QG_F32 && scales_dtype != QG_BF16) return hipErrorInvalidValue;
+  if (!float_dtype(out_dtype) || (bias && !float_dtype(bias_dtype))) return hipErrorInvalidValue;
+  // activation rows are read as 16-byte vectors
+  if (a_sm < k || a_sm % 8 != 0) return hipErrorInvalidValue;
+  if (m == 0) return hipSuccess;
+  if (!a || !w || !scales || !zeros || !out) return hipErrorInvalidValue;
+  if (!aligned16(a) || !aligned16(w)) return hipErrorInvalidValue;
+  if ((m - 1) * a_sm + k >= (int64_t(1) << 40)) return hipErrorInvalidValue;
+  qg::W4Args p{};
+  p.a = static_cast<const uint16_t*>(a);
+  p.a_sm = a_sm;
+  p.a_f16 = a_dtype == QG_F16;
+  p.M = static_cast<int>(m);
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(k);
+  p.w = reinterpret_cast<const uint32_t*>(w);
+  p.flags = flags;
+  p.group = group_size;
+  p.scales = scales;
+  p.scale_f32 = scales_dtype == QG_F32;
+  p.zeros = zeros;
+  p.bias = bias;
+  p.bias_dtype = bias_dtype;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  return qg::launch_w4a16(p, static_cast<hipStream_t>(stream));
+}

@@ -37,4 +37,38 @@ hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t x_sm,
                              int64_t q_sm, int64_t k_pad, float* step,
                              int rounding, hipStream_t stream);
 
+// W4A16 GEMM / unpack operands (see include/qgemm.h for the storage flags).
+struct W4Args {
+  const uint16_t* a;     // activations [M, K] fp16 / bf16, unit K stride
+  int64_t a_sm;
+  int a_f16;             // 1: fp16 activations, 0: bf16
+  int M, N, K;
+  const uint32_t* w;     // packed words, [N, K/8] or [K/8, N]
+  int flags;             // qg_w4_flags
+  int group;             // 32, 64 or 128
+  const void* scales;    // [N, K/G] fp32 or bf16
+  int scale_f32;
+  const void* zeros;     // int32 [N, K/G] or packed uint4 [N, ceil(K/G/8)]
+  const void* bias;      // nullptr or [N] of bias_dtype
+  int bias_dtype;
+  void* out;             // [M, N] contiguous (unpack: [N, K])
+  int out_dtype;
+};
+
+struct W4PackArgs {
+  const void* w;         // [N, K] fp32 / fp16 / bf16, strides in elements
+  int w_dtype;
+  int64_t w_sn, w_sk;
+  int N, K, group, symmetric, flags;
+  int32_t* data;
+  void* scales;
+  int scale_dtype;       // QG_F32 or QG_BF16
+  void* zeros;
+  int32_t* sums;         // nullptr or [N, K/G]
+};
+
+hipError_t launch_w4a16(const W4Args& p, hipStream_t stream);
+hipError_t launch_w4_pack(const W4PackArgs& p, hipStream_t stream);
+hipError_t launch_w4_unpack(const W4Args& p, hipStream_t stream);
+
 }  // namespace qg

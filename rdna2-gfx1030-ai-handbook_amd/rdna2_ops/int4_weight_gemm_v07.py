@@ -1,0 +1,294 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Grouped INT4 weight storage and the W4A16 GEMM on gfx950 (MI355X).
+
+Drop-in for rdna2-ops/rdna2_ops/int4_weight_gemm_v07.py: ``PackedInt4``,
+``pack_int4_cpu`` / ``unpack_int4_cpu``, ``pack_int4``, ``unpack_int4`` and
+``int4_linear_a16`` keep their signatures, argument checks and storage
+format (signed 4-bit q and fp32 scale / int32 zero point per output-row K
+group, W = (q - zero) * scale; linear INT4, never a codebook format). The
+device work runs in hand-written gfx950 HIP kernels of librdna2_qgemm.so
+(C ABI: include/qgemm.h); a missing library is an error.
+
+``int4_linear_a16`` methods:
+  dequant   unpack_int4 (HIP) to fp16/bf16, then the library GEMM F.linear
+            (the reference's "decode + rocBLAS" method);
+  prepared  F.linear with a caller-owned dequantised weight;
+  dot2      the fused kernel: nibbles are expanded in registers and fed to the
+            bf16/fp16 MFMA; each group scale multiplies the exact group partial
+            sum in fp32 (the reference's dot2 rounds each weight to fp16 first).
+  fused     alias of dot2.
+
+Extensions (defaults keep the reference's behaviour): bf16 activations (the
+output and bias then are bf16), and the BASELINE configuration-2 storage
+``pack_uint4`` — unsigned nibbles, bf16 scales, uint4 zero points packed 8 per
+int32 (PackedInt4 with ``signed=False, zeros_packed=True``).
+
+The caller owns packed weights and re-packs them after weight/LoRA changes.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_GROUPS = (32, 64, 128)
+
+
+@dataclass
+class PackedInt4:
+    """Caller-owned W4 weight (int4_weight_gemm_v07.py:20-46).
+
+    ``signed`` / ``zeros_packed`` describe the storage coordinates: the
+    reference format is signed=True, zeros_packed=False (int32 zero points);
+    the BASELINE uint4 format is signed=False, zeros_packed=True."""
+    data: torch.Tensor
+    scales: torch.Tensor
+    zeros: torch.Tensor
+    sums: torch.Tensor
+    n: int
+    k: int
+    group_size: int
+    symmetric: bool
+    layout: str = "nk"
+    order: str = "low"
+    signed: bool = True
+    zeros_packed: bool = False
+
+    def to(self, device):
+        return PackedInt4(*(t.to(device) for t in (self.data, self.scales, self.zeros, self.sums)),
+                          self.n, self.k, self.group_size, self.symmetric, self.layout, self.order,
+                          self.signed, self.zeros_packed)
+
+    @property
+    def bytes(self):
+        return sum(t.numel() * t.element_size() for t in (self.data, self.scales, self.zeros, self.sums))
+
+    @property
+    def logical_stride(self):
+        return self.data.stride() if self.layout == "nk" else self.data.T.stride()
+
+    @property
+    def flags(self):
+        f = 0
+        if self.signed:
+            f |= _lib.W4_SIGNED_NIBBLES
+        if self.order == "high":
+            f |= _lib.W4_ORDER_HIGH
+        if self.layout == "kn":
+            f |= _lib.W4_LAYOUT_KN
+        if self.zeros_packed:
+            f |= _lib.W4_ZEROS_PACKED
+        return f
+
+
+# ------------------------------------------------------------------ CPU packing
+def _shifts(order):
+    s = torch.arange(8, dtype=torch.int64) * 4
+    return 28 - s if order == "high" else s
+
+
+def pack_int4_cpu(w, *, group_size=64, symmetric=True, layout="nk", order="low"):
+    """CPU packing with ties-to-even and an explicit range
+    (int4_weight_gemm_v07.py:49-82); the GPU pack_int4 must equal it."""
+    if w.device.type != "cpu" or w.ndim != 2 or not w.is_floating_point():
+        raise ValueError("CPU floating-point [N,K] weight required")
+    n, k = w.shape
+    if group_size not in _GROUPS or k % group_size or layout not in ("nk", "kn") or order not in ("low", "high"):
+        raise ValueError("K must be divisible by group size 32/64/128; valid layout/order required")
+    if not torch.isfinite(w).all():
+        raise ValueError("Finite weight required")
+    x = w.float().reshape(n, k // group_size, group_size)
+    if symmetric:
+        scales = x.abs().amax(-1) / 7
+        scales = torch.where(scales == 0, torch.ones_like(scales), scales)
+        zeros = torch.zeros_like(scales, dtype=torch.int32)
+        q = torch.round(x / scales[..., None]).clamp(-7, 7).to(torch.int32)
+    else:
+        zero = torch.zeros((), dtype=torch.float32)
+        lo = torch.minimum(x.amin(-1), zero)
+        hi = torch.maximum(x.amax(-1), zero)
+        scales = (hi - lo) / 15
+        empty = scales == 0
+        scales = torch.where(empty, torch.ones_like(scales), scales)
+        zu = torch.round(-lo / scales).clamp(0, 15).to(torch.int32)
+        zeros = torch.where(empty, torch.zeros_like(zu), zu - 8)
+        q = (torch.round(x / scales[..., None]) + zu[..., None]).clamp(0, 15).to(torch.int32) - 8
+        q = torch.where(empty[..., None], torch.zeros_like(q), q)
+    sums = q.sum(-1, dtype=torch.int32)
+    nib = q.reshape(n, k // 8, 8).to(torch.int64) & 15
+    words = (nib << _shifts(order)).sum(-1)
+    words = torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)
+    if layout == "kn":
+        words = words.T.contiguous()
+    return PackedInt4(words, scales.contiguous(), zeros.contiguous(), sums.contiguous(),
+                      n, k, group_size, bool(symmetric), layout, order)
+
+
+def unpack_int4_cpu(p, *, floating=True):
+    """(q - zero) * scale as fp32 [N, K], or the centred integers
+    (int4_weight_gemm_v07.py:85-92)."""
+    words = p.data.cpu() if p.layout == "nk" else p.data.cpu().T
+    nib = ((words.to(torch.int64)[..., None] >> _shifts(p.order)) & 15).to(torch.int32)
+    nib = nib.reshape(p.n, p.k // p.group_size, p.group_size)
+    if p.signed:
+        q = torch.where(nib >= 8, nib - 16, nib)
+    else:
+        q = nib
+    if p.zeros_packed:
+        ng = p.k // p.group_size
+        zw = p.zeros.cpu().to(torch.int64)
+        zn = ((zw[..., None] >> (torch.arange(8, dtype=torch.int64) * 4)) & 15).reshape(p.n, -1)[:, :ng]
+        z = torch.where(zn >= 8, zn - 16, zn) if p.signed else zn
+        z = z.to(torch.int32)
+    else:
+        z = p.zeros.cpu()
+    centred = q - z[..., None]
+    if not floating:
+        return centred.reshape(p.n, p.k)
+    return (centred.float() * p.scales.cpu().float()[..., None]).reshape(p.n, p.k)
+
+
+# ------------------------------------------------------------------ device API
+def _eager(*tensors):
+    if (torch.compiler.is_compiling() or torch.cuda.is_current_stream_capturing()
+            or torch.is_autocast_enabled("cuda") or torch.jit.is_tracing()
+            or torch._C._are_functorch_transforms_active()
+            or torch.is_grad_enabled() and any(t.requires_grad for t in tensors)):
+        raise ValueError("Explicit eager inference only")
+
+
+def _storage(n, k, group_size, layout, signed, zeros_packed, scale_dtype, device):
+    data = torch.empty((n, k // 8) if layout == "nk" else (k // 8, n), device=device, dtype=torch.int32)
+    scales = torch.empty((n, k // group_size), device=device, dtype=scale_dtype)
+    ng = k // group_size
+    zeros = torch.empty((n, (ng + 7) // 8) if zeros_packed else (n, ng), device=device, dtype=torch.int32)
+    sums = torch.empty((n, ng), device=device, dtype=torch.int32)
+    return data, scales, zeros, sums
+
+
+def _pack(w, group_size, symmetric, layout, order, signed, zeros_packed, scale_dtype):
+    if w.device.type != "cuda" or w.ndim != 2 or not w.is_floating_point():
+        raise ValueError("Floating [N,K] weight on gfx950 required")
+    _lib.require_gfx950(w)
+    _eager(w)
+    n, k = w.shape
+    if group_size not in _GROUPS or k % group_size or min(n, k) <= 0 or n * k >= 2 ** 31:
+        raise ValueError("Nonempty bounded shape and K divisible by 32/64/128 required")
+    if layout not in ("nk", "kn") or order not in ("low", "high"):
+        raise ValueError("Unknown packing layout/order")
+    if min(w.stride()) <= 0:
+        raise ValueError("Positive strides required")
+    if w.dtype not in _lib.DTYPE_CODE or _lib.DTYPE_CODE[w.dtype] not in (_lib.F32, _lib.F16, _lib.BF16):
+        raise ValueError("fp32 / fp16 / bf16 weight required")
+    data, scales, zeros, sums = _storage(n, k, group_size, layout, signed, zeros_packed, scale_dtype, w.device)
+    p = PackedInt4(data, scales, zeros, sums, n, k, group_size, bool(symmetric), layout, order,
+                   signed, zeros_packed)
+    _lib.check(_lib.library().qg_w4_pack(
+        _lib.ptr(w), _lib.DTYPE_CODE[w.dtype], w.stride(0), w.stride(1), n, k, group_size,
+        int(bool(symmetric)), p.flags, _lib.ptr(data), _lib.ptr(scales), _lib.DTYPE_CODE[scale_dtype],
+        _lib.ptr(zeros), _lib.ptr(sums), _lib.stream_of(w)), "qg_w4_pack")
+    return p
+
+
+def pack_int4(w, *, group_size=64, symmetric=True, layout="nk", order="low"):
+    """GPU packing, equal to pack_int4_cpu (int4_weight_gemm_v07.py:413-430)."""
+    return _pack(w, group_size, symmetric, layout, order, True, False, torch.float32)
+
+
+def pack_uint4(w, *, group_size=128):
+    """BASELINE configuration-2 storage: asymmetric, unsigned nibbles (nk, low
+    order), bf16 scales (the scale is rounded to bf16 before the codes are
+    computed) and uint4 zero points packed 8 per int32 along the groups."""
+    return _pack(w, group_size, False, "nk", "low", False, True, torch.bfloat16)
+
+
+def _validate(p):
+    """Contract of int4_weight_gemm_v07.py:433-447 (arch: gfx950)."""
+    if not isinstance(p, PackedInt4) or p.data.device.type != "cuda":
+        raise ValueError("PackedInt4 on gfx950 required")
+    _lib.require_gfx950(p.data)
+    if (p.group_size not in _GROUPS or min(p.n, p.k) <= 0 or p.k % p.group_size or p.n * p.k >= 2 ** 31
+            or p.layout not in ("nk", "kn") or p.order not in ("low", "high")
+            or p.data.dtype != torch.int32 or not p.data.is_contiguous()
+            or tuple(p.data.shape) != ((p.n, p.k // 8) if p.layout == "nk" else (p.k // 8, p.n))):
+        raise ValueError("Invalid packed shape/storage")
+    ng = p.k // p.group_size
+    zshape = (p.n, (ng + 7) // 8) if p.zeros_packed else (p.n, ng)
+    scale_dtypes = (torch.float32, torch.bfloat16)
+    for t, dtypes, shape in ((p.scales, scale_dtypes, (p.n, ng)), (p.zeros, (torch.int32,), zshape),
+                             (p.sums, (torch.int32,), (p.n, ng))):
+        if t.device != p.data.device or t.dtype not in dtypes or tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError("Invalid scale/zero/sum storage")
+    if p.data.data_ptr() % 16:
+        raise ValueError("Packed words must be 16-byte aligned")
+    _eager(p.data, p.scales)
+
+
+def unpack_int4(p, *, dtype=torch.float16):
+    """(q - zero) * scale rounded once to ``dtype`` (fp16 / fp32 / bf16), or the
+    centred integers (int8) — int4_weight_gemm_v07.py:450-458."""
+    _validate(p)
+    if dtype not in (torch.float16, torch.float32, torch.bfloat16, torch.int8):
+        raise TypeError(dtype)
+    out = torch.empty((p.n, p.k), device=p.data.device, dtype=dtype)
+    _lib.check(_lib.library().qg_w4_unpack(
+        _lib.ptr(p.data), p.n, p.k, p.group_size, p.flags, _lib.ptr(p.scales),
+        _lib.DTYPE_CODE[p.scales.dtype], _lib.ptr(p.zeros), _lib.ptr(out), _lib.DTYPE_CODE[dtype],
+        _lib.stream_of(p.data)), "qg_w4_unpack")
+    return out
+
+
+def w4a16_gemm(a, p, bias=None, *, out_dtype=None):
+    """The fused W4A16 kernel: out = a @ dequant(p)^T (+ bias), fp32
+    accumulation, one rounding to out_dtype (default: a's dtype)."""
+    m, k = a.shape
+    out_dtype = a.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError("out_dtype must be float16, bfloat16 or float32")
+    if a.stride(1) != 1 or a.stride(0) % 8 or a.data_ptr() % 16:
+        a = a.contiguous()
+    out = torch.empty((m, p.n), device=a.device, dtype=out_dtype)
+    if m == 0:
+        return out
+    lib = _lib.library()
+    ws_bytes = lib.qg_w4a16_gemm_workspace_bytes(m, p.n, k, p.group_size, p.flags)
+    wsp, wsn = _lib.ws_ptr(_lib.workspace(ws_bytes, a.device))
+    _lib.check(lib.qg_w4a16_gemm(
+        _lib.ptr(a), _lib.DTYPE_CODE[a.dtype], a.stride(0), m, k, _lib.ptr(p.data), p.n, p.group_size,
+        p.flags, _lib.ptr(p.scales), _lib.DTYPE_CODE[p.scales.dtype], _lib.ptr(p.zeros), _lib.ptr(bias),
+        _lib.DTYPE_CODE[bias.dtype] if bias is not None else 0, _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
+        wsp, wsn, _lib.stream_of(a)), "qg_w4a16_gemm")
+    return out
+
+
+def int4_linear_a16(a, p, *, bias=None, method="dequant", prepared=None, tile=(64, 64, 32),
+                    num_warps=4, return_kernel=False):
+    """fp16 (or bf16) activation and output: decode + library GEMM, prepared
+    library GEMM, or the fused dot2 kernel (int4_weight_gemm_v07.py:540-564)."""
+    _validate(p)
+    _eager(a)
+    if a.dtype not in (torch.float16, torch.bfloat16) or a.ndim != 2 or a.shape[1] != p.k or a.device != p.data.device:
+        raise ValueError("Matching FP16 activation [M,K] required")
+    if min(a.stride()) <= 0 or a.shape[0] * p.n >= 2 ** 31:
+        raise ValueError("Unsupported shape/stride")
+    if bias is not None and (bias.dtype != a.dtype or bias.shape != (p.n,) or bias.device != a.device):
+        raise ValueError("FP16 bias [N] required")
+    if method in ("dequant", "prepared"):
+        w = unpack_int4(p, dtype=a.dtype) if method == "dequant" else prepared
+        if w is None or w.shape != (p.n, p.k) or w.dtype != a.dtype or w.device != a.device:
+            raise ValueError("FP16 prepared weight required")
+        result = torch.nn.functional.linear(a, w, bias)
+        return (result, None) if return_kernel else result
+    if method not in ("dot2", "fused"):
+        raise ValueError(method)
+    if len(tile) != 3 or any(x not in (16, 32, 64, 128) for x in tile) or p.k % tile[2]:
+        raise ValueError("Supported dot2 tile required")
+    if bias is not None and not bias.is_contiguous():
+        bias = bias.contiguous()
+    out = w4a16_gemm(a, p, bias)
+    if return_kernel:
+        fm = 1 if a.shape[0] <= 16 else 2 if a.shape[0] <= 32 else 4
+        return out, _lib.kernel_metadata("w4a16_skinny", (16 * fm, 16, 128), "k_w4_skinny")
+    return out

@@ -296,6 +296,8 @@ extern "C" int qg_w4_unpack(const int32_t* data, int64_t n, int64_t k, int group
   p.w = reinterpret_cast<const uint32_t*>(data);
   p.flags = flags;
   p.group = group_size;
+  p.ng = static_cast<int>(k / group_size);
+  p.zw = (p.ng + 7) / 8;
   p.scales = scales;
   p.scale_f32 = scales_dtype == QG_F32;
   p.zeros = zeros;
@@ -331,7 +333,8 @@ extern "C" int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m
   if (m == 0) return hipSuccess;
   if (!a || !w || !scales || !zeros || !out) return hipErrorInvalidValue;
   if (!aligned16(a) || !aligned16(w)) return hipErrorInvalidValue;
-  if ((m - 1) * a_sm + k >= (int64_t(1) << 40)) return hipErrorInvalidValue;
+  // activation addresses are 32-bit byte offsets from the base
+  if ((m - 1) * a_sm + k >= (int64_t(1) << 31)) return hipErrorInvalidValue;
   qg::W4Args p{};
   p.a = static_cast<const uint16_t*>(a);
   p.a_sm = a_sm;
@@ -342,6 +345,8 @@ extern "C" int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m
   p.w = reinterpret_cast<const uint32_t*>(w);
   p.flags = flags;
   p.group = group_size;
+  p.ng = static_cast<int>(k / group_size);
+  p.zw = (p.ng + 7) / 8;
   p.scales = scales;
   p.scale_f32 = scales_dtype == QG_F32;
   p.zeros = zeros;

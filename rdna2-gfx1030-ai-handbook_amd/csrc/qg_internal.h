@@ -46,6 +46,8 @@ struct W4Args {
   const uint32_t* w;     // packed words, [N, K/8] or [K/8, N]
   int flags;             // qg_w4_flags
   int group;             // 32, 64 or 128
+  int ng;                // groups per row, K / group
+  int zw;                // packed zero-point words per row, ceil(ng / 8)
   const void* scales;    // [N, K/G] fp32 or bf16
   int scale_f32;
   const void* zeros;     // int32 [N, K/G] or packed uint4 [N, ceil(K/G/8)]

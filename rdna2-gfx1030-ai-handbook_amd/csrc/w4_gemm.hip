@@ -18,6 +18,8 @@
 #include "qg_common.h"
 #include "qg_internal.h"
 
+#include <stdlib.h>
+
 namespace qg {
 
 namespace {
@@ -47,12 +49,14 @@ __device__ __forceinline__ f32x4 mfma16(const i32x4& a, const i32x4& b, const f3
 // keeps the nibbles and inserts the exponent.
 // bf16: nibbles land in bits 0-3 of each half (bytes of w and w >> 4);
 // fp16: in bits 4-7 (bytes of w << 4 and w).
+// mask / magic2 come from unpack_consts(): held in registers so that each
+// register costs one v_perm_b32 and one v_and_or_b32 (a VOP3 instruction
+// cannot take the literals directly on gfx9).
 template <bool F16A>
-__device__ __forceinline__ i32x4 unpack_word(uint32_t w, const uint32_t (&sel)[4]) {
+__device__ __forceinline__ i32x4 unpack_word(uint32_t w, const uint32_t (&sel)[4], uint32_t mask,
+                                             uint32_t magic2) {
   const uint32_t lo = F16A ? w << 4 : w;
   const uint32_t hi = F16A ? w : w >> 4;
-  constexpr uint32_t mask = F16A ? 0x00F000F0u : 0x000F000Fu;
-  constexpr uint32_t magic2 = F16A ? 0x5C005C00u : 0x43004300u;  // fp16 256 / bf16 128
   i32x4 r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -60,6 +64,13 @@ __device__ __forceinline__ i32x4 unpack_word(uint32_t w, const uint32_t (&sel)[4
     r[i] = static_cast<int>((t & mask) | magic2);
   }
   return r;
+}
+
+template <bool F16A>
+__device__ __forceinline__ void unpack_consts(uint32_t& mask, uint32_t& magic2) {
+  mask = F16A ? 0x00F000F0u : 0x000F000Fu;
+  magic2 = F16A ? 0x5C005C00u : 0x43004300u;  // fp16 256 / bf16 128
+  asm volatile("" : "+v"(mask), "+v"(magic2));
 }
 
 // v_perm selectors: combined bytes 0-3 = lo, 4-7 = hi (lo/hi: the two shifted
@@ -90,42 +101,79 @@ __device__ __forceinline__ void store_out(void* out, int dtype, int64_t idx, flo
 }
 
 // Scale and unsigned zero point of group g of column n, in the units of the
-// expanded weights: weight value = (zb_unit * u + magic) with zb = magic +
-// unit * zu and s = scale / unit (unit 4 for fp16, 1 otherwise; exact).
+// expanded weights (value = magic + unit * u): zb = magic + unit * zu and
+// s = scale / unit (unit 4 for fp16, 1 for bf16; exact).
 struct GroupParams {
   float s, zb;
 };
 
-__device__ __forceinline__ GroupParams group_params(const W4Args& p, int n, int g, float magic,
-                                                    float unit = 1.0f) {
-  const int ng = p.K / p.group;
-  GroupParams r;
-  const int64_t i = static_cast<int64_t>(n) * ng + g;
-  r.s = p.scale_f32 ? static_cast<const float*>(p.scales)[i]
-                    : bf16_to_f32(static_cast<const uint16_t*>(p.scales)[i]);
-  int zu;
-  if (p.flags & QG_W4_ZEROS_PACKED) {
-    const int zw = (ng + 7) >> 3;
-    const uint32_t word = static_cast<const uint32_t*>(p.zeros)[static_cast<int64_t>(n) * zw + (g >> 3)];
-    zu = static_cast<int>((word >> ((g & 7) * 4)) & 15u);
-    if (p.flags & QG_W4_SIGNED_NIBBLES) zu ^= 8;
-  } else {
-    zu = static_cast<const int32_t*>(p.zeros)[i];
-    if (p.flags & QG_W4_SIGNED_NIBBLES) zu += 8;
-  }
-  r.zb = magic + unit * static_cast<float>(zu);
-  r.s = r.s / unit;
+// Raw storage words of a group's scale and zero point. Both are read as
+// aligned dwords whatever the storage dtype, so the loads are unconditional
+// (no data-dependent control flow around them); the dtype and packing are
+// resolved afterwards by decode_group().
+struct GroupRaw {
+  uint32_t s, z;
+};
+
+__device__ __forceinline__ GroupRaw load_group(const W4Args& p, int n, int g) {
+  const uint32_t i = static_cast<uint32_t>(n) * p.ng + g;
+  const uint32_t sb = p.scale_f32 ? 4u * i : 4u * (i >> 1);
+  const uint32_t zb = (p.flags & QG_W4_ZEROS_PACKED)
+                          ? 4u * (static_cast<uint32_t>(n) * p.zw + (g >> 3))
+                          : 4u * i;
+  GroupRaw r;
+  r.s = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.scales) + sb);
+  r.z = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.zeros) + zb);
   return r;
 }
 
+// UINT4: storage known at compile time to be bf16 scales, packed unsigned
+// zero points (the BASELINE format); otherwise resolved from p.flags.
+template <bool UINT4 = false>
+__device__ __forceinline__ GroupParams decode_group(const W4Args& p, GroupRaw raw, int n, int g,
+                                                    float magic, float unit) {
+  const uint32_t i = static_cast<uint32_t>(n) * p.ng + g;
+  if constexpr (UINT4) {
+    GroupParams r;
+    r.s = __uint_as_float((i & 1u) ? (raw.s & 0xFFFF0000u) : (raw.s << 16)) / unit;
+    r.zb = magic + unit * static_cast<float>((raw.z >> ((g & 7) * 4)) & 15u);
+    return r;
+  }
+  const uint32_t sbits = p.scale_f32 ? raw.s : ((i & 1u) ? (raw.s & 0xFFFF0000u) : (raw.s << 16));
+  const bool packed = p.flags & QG_W4_ZEROS_PACKED;
+  const bool sgn = p.flags & QG_W4_SIGNED_NIBBLES;
+  const int z = packed ? static_cast<int>((raw.z >> ((g & 7) * 4)) & 15u) : static_cast<int>(raw.z);
+  const int zu = sgn ? (packed ? (z ^ 8) : z + 8) : z;
+  GroupParams r;
+  r.s = __uint_as_float(sbits) / unit;
+  r.zb = magic + unit * static_cast<float>(zu);
+  return r;
+}
+
+__device__ __forceinline__ GroupParams group_params(const W4Args& p, int n, int g, float magic,
+                                                    float unit = 1.0f) {
+  return decode_group(p, load_group(p, n, g), n, g, magic, unit);
+}
+
 // ------------------------------------------------------------- skinny kernel
-// Small M (decode): one 256-thread workgroup per 16 output columns x 16*FM
-// rows. The K axis is cut into 128-wide chunks; wave w takes chunks
-// w, w+4, w+8, ... so the four waves stream each weight row front to back
-// together. Per chunk a lane loads its column's 4 words (16 bytes, one
-// dwordx4 in the nk / group-128 layout) and its rows' activations straight
-// from memory; no LDS staging, DEPTH chunks in flight per wave. The four
-// partial tiles are summed through LDS in a fixed order (deterministic).
+// Small M (decode): one workgroup of WAVES waves per 16*CT output columns x
+// 16*FM rows. The K axis is cut into 128-wide chunks; wave w takes chunks
+// w, w+WAVES, ... so the waves stream each weight row front to back
+// together. Per chunk a lane loads, for each of its CT column tiles, its
+// column's 4 words (16 bytes, one dwordx4 in the nk / group-128 layout), and
+// once the activation fragments of its rows, which all CT tiles share (as
+// does the MFMA against ones that yields the per-row group sums). No LDS
+// staging; DEPTH chunks in flight per wave. The WAVES partial tiles are summed
+// through LDS in a fixed order (deterministic).
+//
+// Every load is unconditional, addressed with a 32-bit byte offset from a
+// wave-uniform base and clamped into its tensor: activation rows past M
+// repeat row M-1 (they only reach output rows that are not stored), columns
+// past N repeat column N-1, steps past K re-read the last valid words, and
+// refills past a wave's last chunk re-read that chunk (a cache hit); such
+// groups are computed with scale 0. Conditional loads, or branches around
+// the MFMAs, would make the compiler wait for all outstanding loads (or copy
+// the accumulators) at every join.
 //
 // Word f of a chunk feeds MFMA step j from lane group q, with f chosen so
 // that each step stays inside one quantisation group:
@@ -139,15 +187,20 @@ __device__ __forceinline__ int word_of(int q, int j) {
   else return 4 * j + q;
 }
 
-template <int FM, int SPC>
+template <int FM, int CT, int SPC>
 struct SkinnyChunk {
-  uint32_t w[4];
+  uint32_t w[CT][4];
   i32x4 a[FM][4];
-  GroupParams gp[SPC];
+  GroupRaw gr[CT][SPC];
 };
 
-template <int FM, int G, bool KN, bool F16A, int DEPTH>
-__global__ __launch_bounds__(256) void k_w4_skinny(W4Args p) {
+template <typename T>
+__device__ __forceinline__ T load_at(const void* base, uint32_t byte_off) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off);
+}
+
+template <int FM, int CT, int G, bool KN, bool F16A, int DEPTH, int WAVES, bool UINT4>
+__global__ __launch_bounds__(64 * WAVES) void k_w4_skinny(W4Args p) {
 #pragma clang fp contract(off)
   constexpr int SPC = 128 / G;                  // groups per chunk
   constexpr int STEPS_PER_GROUP = 4 / SPC;
@@ -155,87 +208,99 @@ __global__ __launch_bounds__(256) void k_w4_skinny(W4Args p) {
   constexpr float UNIT = F16A ? 4.0f : 1.0f;
   const uint32_t ones2 = F16A ? 0x3C003C00u : 0x3F803F80u;
 
-  __shared__ float red[4][FM * 16][17];
+  __shared__ float red[WAVES][FM * 16][CT * 16 + 1];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15, q = lane >> 4;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * CT;
   const int m0 = blockIdx.y * 16 * FM;
-  const int n = min(n0 + col, p.N - 1);
+  int ncol[CT];
+  static_for<0, CT>([&](auto t) { ncol[t] = min(n0 + 16 * t + col, p.N - 1); });
   const int C = ceil_div(p.K, 128);
   const int KW = p.K >> 3;  // words per column
+  // last chunk of this wave (a wave without chunks re-reads chunk 0)
+  const int clast = wave < C ? wave + WAVES * ((C - 1 - wave) / WAVES) : 0;
 
   uint32_t sel[4];
   unpack_selectors(p.flags & QG_W4_ORDER_HIGH, sel);
-  const uint32_t wxor = (p.flags & QG_W4_SIGNED_NIBBLES) ? 0x88888888u : 0u;
+  const uint32_t wxor = (!UINT4 && (p.flags & QG_W4_SIGNED_NIBBLES)) ? 0x88888888u : 0u;
+  uint32_t umask, umagic;
+  unpack_consts<F16A>(umask, umagic);
   const i32x4 ones = {static_cast<int>(ones2), static_cast<int>(ones2), static_cast<int>(ones2),
                       static_cast<int>(ones2)};
 
-  const uint32_t* wcol = KN ? p.w + n : p.w + static_cast<int64_t>(n) * KW;
-  const int64_t wstride = KN ? p.N : 1;
+  // byte offset of word kw of column n
+  auto woff = [&](int n, int kw) -> uint32_t {
+    return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (static_cast<uint32_t>(n) * KW + kw);
+  };
+  uint32_t arow_off[FM];
+  static_for<0, FM>([&](auto f) {
+    arow_off[f] = 2u * static_cast<uint32_t>(min(m0 + 16 * f + col, p.M - 1)) * static_cast<uint32_t>(p.a_sm);
+  });
 
-  auto load = [&](SkinnyChunk<FM, SPC>& ch, int c) {
+  auto load = [&](SkinnyChunk<FM, CT, SPC>& ch, int c) {
     const int kw0 = c * 16;
-    const int steps = min(4, (p.K - c * 128) >> 5);
-    if constexpr (!KN && G == 128) {
-      const i32x4 v = *reinterpret_cast<const i32x4*>(wcol + kw0 + 4 * q);
-      static_for<0, 4>([&](auto j) { ch.w[j] = static_cast<uint32_t>(v[int(j)]); });
-    } else if constexpr (!KN && G == 64) {
-      const uint2 v0 = *reinterpret_cast<const uint2*>(wcol + kw0 + 2 * q);
-      ch.w[0] = v0.x;
-      ch.w[1] = v0.y;
-      if (steps > 2) {
-        const uint2 v1 = *reinterpret_cast<const uint2*>(wcol + kw0 + 8 + 2 * q);
-        ch.w[2] = v1.x;
-        ch.w[3] = v1.y;
+    static_for<0, CT>([&](auto t) {
+      const int n = ncol[t];
+      if constexpr (!KN && G == 128) {
+        const i32x4 v = load_at<i32x4>(p.w, woff(n, kw0 + 4 * q));
+        static_for<0, 4>([&](auto j) { ch.w[t][j] = static_cast<uint32_t>(v[int(j)]); });
+      } else if constexpr (!KN && G == 64) {
+        const uint2 v0 = load_at<uint2>(p.w, woff(n, kw0 + 2 * q));
+        const uint2 v1 = load_at<uint2>(p.w, woff(n, min(kw0 + 8 + 2 * q, KW - 2)));
+        ch.w[t][0] = v0.x;
+        ch.w[t][1] = v0.y;
+        ch.w[t][2] = v1.x;
+        ch.w[t][3] = v1.y;
       } else {
-        ch.w[2] = ch.w[3] = 0;
+        static_for<0, 4>([&](auto j) {
+          ch.w[t][j] = load_at<uint32_t>(p.w, woff(n, min(kw0 + word_of<G, KN>(q, j), KW - 1)));
+        });
       }
-    } else {
-      static_for<0, 4>([&](auto j) {
-        ch.w[j] = j < steps ? wcol[(kw0 + word_of<G, KN>(q, j)) * wstride] : 0u;
-      });
-    }
-    static_for<0, SPC>([&](auto g) {
-      if (g * (G / 32) < steps) ch.gp[g] = group_params(p, n, c * SPC + g, MAGIC, UNIT);
+      static_for<0, SPC>([&](auto g) { ch.gr[t][g] = load_group(p, n, min(c * SPC + g, p.ng - 1)); });
     });
     static_for<0, FM>([&](auto f) {
-      const int row = m0 + 16 * f + col;
-      const uint16_t* arow = p.a + static_cast<int64_t>(min(row, p.M - 1)) * p.a_sm + c * 128;
       static_for<0, 4>([&](auto j) {
-        i32x4 v = {0, 0, 0, 0};
-        if (row < p.M && j < steps)
-          v = *reinterpret_cast<const i32x4*>(arow + 8 * word_of<G, KN>(q, j));
-        ch.a[f][j] = v;
+        const int k = min(c * 128 + 8 * word_of<G, KN>(q, j), p.K - 8);
+        ch.a[f][j] = load_at<i32x4>(p.a, arow_off[f] + 2u * k);
       });
     });
   };
 
-  f32x4 total[FM], acc[FM], asum[FM];
-  static_for<0, FM>([&](auto f) { total[f] = f32x4{0, 0, 0, 0}; });
+  f32x4 total[CT][FM], acc[CT][FM], asum[FM];
+  static_for<0, CT>([&](auto t) {
+    static_for<0, FM>([&](auto f) { total[t][f] = f32x4{0, 0, 0, 0}; });
+  });
 
-  auto compute = [&](const SkinnyChunk<FM, SPC>& ch, int c) {
-    const int steps = min(4, (p.K - c * 128) >> 5);
+  // Straight-line: all 4 steps of every scheduled chunk run on (clamped)
+  // data; a group that does not exist — past K, or a refill past the wave's
+  // last chunk — gets scale 0 and adds exactly 0 (inputs are finite).
+  auto compute = [&](const SkinnyChunk<FM, CT, SPC>& ch, int c) {
+    const bool live = c <= clast;
     static_for<0, 4>([&](auto j) {
-      if (j < steps) {
+      {
         if constexpr (j % STEPS_PER_GROUP == 0) {
           static_for<0, FM>([&](auto f) {
-            acc[f] = f32x4{0, 0, 0, 0};
             asum[f] = f32x4{0, 0, 0, 0};
+            static_for<0, CT>([&](auto t) { acc[t][f] = f32x4{0, 0, 0, 0}; });
           });
         }
-        const i32x4 b = unpack_word<F16A>(ch.w[j] ^ wxor, sel);
-        static_for<0, FM>([&](auto f) {
-          acc[f] = mfma16<F16A>(ch.a[f][j], b, acc[f]);
-          asum[f] = mfma16<F16A>(ch.a[f][j], ones, asum[f]);
+        static_for<0, FM>([&](auto f) { asum[f] = mfma16<F16A>(ch.a[f][j], ones, asum[f]); });
+        static_for<0, CT>([&](auto t) {
+          const i32x4 b = unpack_word<F16A>(UINT4 ? ch.w[t][j] : ch.w[t][j] ^ wxor, sel, umask, umagic);
+          static_for<0, FM>([&](auto f) { acc[t][f] = mfma16<F16A>(ch.a[f][j], b, acc[t][f]); });
         });
         if constexpr (j % STEPS_PER_GROUP == STEPS_PER_GROUP - 1) {
-          const GroupParams gp = ch.gp[j / STEPS_PER_GROUP];
-          static_for<0, FM>([&](auto f) {
-            static_for<0, 4>([&](auto i) {
-              const float t = acc[f][int(i)] - gp.zb * asum[f][int(i)];
-              total[f][int(i)] = total[f][int(i)] + gp.s * t;
+          constexpr int gi = j / STEPS_PER_GROUP;
+          static_for<0, CT>([&](auto t) {
+            GroupParams gp = decode_group<UINT4>(p, ch.gr[t][gi], ncol[t], c * SPC + gi, MAGIC, UNIT);
+            if (!live || c * SPC + gi >= p.ng) gp.s = 0.0f;
+            static_for<0, FM>([&](auto f) {
+              static_for<0, 4>([&](auto i) {
+                const float v = __builtin_fmaf(-gp.zb, asum[f][int(i)], acc[t][f][int(i)]);
+                total[t][f][int(i)] = __builtin_fmaf(gp.s, v, total[t][f][int(i)]);
+              });
             });
           });
         }
@@ -243,34 +308,434 @@ __global__ __launch_bounds__(256) void k_w4_skinny(W4Args p) {
     });
   };
 
-  SkinnyChunk<FM, SPC> buf[DEPTH];
-  static_for<0, DEPTH>([&](auto d) {
-    if (wave + 4 * d < C) load(buf[d], wave + 4 * d);
-  });
-  for (int base = wave; base < C; base += 4 * DEPTH) {
+  SkinnyChunk<FM, CT, SPC> buf[DEPTH];
+  static_for<0, DEPTH>([&](auto d) { load(buf[d], min(wave + WAVES * d, clast)); });
+  for (int base = wave; base <= clast; base += WAVES * DEPTH) {
     static_for<0, DEPTH>([&](auto d) {
-      const int c = base + 4 * d;
-      if (c < C) {
-        compute(buf[d], c);
-        if (c + 4 * DEPTH < C) load(buf[d], c + 4 * DEPTH);
-      }
+      const int c = base + WAVES * d;
+      compute(buf[d], c);
+      load(buf[d], min(c + WAVES * DEPTH, clast));
     });
   }
 
-  static_for<0, FM>([&](auto f) {
-    static_for<0, 4>([&](auto i) { red[wave][16 * f + 4 * q + i][col] = total[f][int(i)]; });
+  static_for<0, CT>([&](auto t) {
+    static_for<0, FM>([&](auto f) {
+      static_for<0, 4>([&](auto i) { red[wave][16 * f + 4 * q + i][16 * t + col] = total[t][f][int(i)]; });
+    });
   });
   __syncthreads();
-  for (int e = threadIdx.x; e < FM * 256; e += 256) {
-    const int r = e >> 4, cc = e & 15;
+  for (int e = threadIdx.x; e < FM * CT * 256; e += 64 * WAVES) {
+    const int r = e / (16 * CT), cc = e % (16 * CT);
     const int row = m0 + r, nn = n0 + cc;
     if (row < p.M && nn < p.N) {
       float v = red[0][r][cc];
-      v = v + red[1][r][cc];
-      v = v + red[2][r][cc];
-      v = v + red[3][r][cc];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) v = v + red[w][r][cc];
       if (p.bias) v = v + load_bias(p.bias, p.bias_dtype, nn);
       store_out(p.out, p.out_dtype, static_cast<int64_t>(row) * p.N + nn, v);
+    }
+  }
+}
+
+// ------------------------------------------------------------- decode kernel
+// M <= 16 (token decode), the HBM-bound shape. One workgroup of WAVES waves
+// per 16*CT output columns; wave w owns a contiguous range of 128-wide K
+// chunks (at most kDecodeChunks). At the start each wave copies its
+// activation slice [rows, 128 * chunks] into its own LDS region (one 16-byte
+// load and one 16-byte LDS store per lane per row and 512 K), storing every
+// 8-element group in the order (0 2 4 6 1 3 5 7). In that order a weight
+// word needs only 7 VALU operations to become 4 MFMA registers:
+//   E = even nibbles as bytes, O = odd nibbles as bytes (one AND, one
+//   shift+AND), then 4 v_perm_b32 that pair two nibble bytes with the
+//   exponent byte of the magic number (bf16 0x43.. = 128 + u, fp16 0x5C.. =
+//   256 + 4u with the nibble placed in bits 4-7).
+// The activation fragments (ds_read_b128) and the MFMA against ones that
+// yields the row sums per group are shared by the CT column tiles. All
+// weight, scale and zero-point loads of a wave are issued before its first
+// MFMA (the chunk range is at most kDecodeChunks long), unconditionally and
+// clamped as in the skinny kernel; the WAVES partial tiles are summed through
+// LDS in a fixed order.
+constexpr int kDecodeChunks = 4;
+
+template <bool F16A, bool UINT4>
+struct Unpack7 {
+  uint32_t mask_e, magic4, sel_a, sel_b, sh_e, sh_o;
+  __device__ __forceinline__ void init(bool high) {
+    mask_e = F16A ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    magic4 = F16A ? 0x5C5C5C5Cu : 0x43434343u;
+    // result bytes (low to high): nibble byte, magic, nibble byte, magic;
+    // combined source bytes 0-3 = E or O, 4-7 = magic. High order keeps the
+    // nibbles of each word in reverse, so its selectors read bytes 3..0 and
+    // the even / odd roles of the two nibbles of a byte swap.
+    sel_a = high ? 0x04020403u : 0x04010400u;
+    sel_b = high ? 0x04000401u : 0x04030402u;
+    // E = nibbles 0,2,4,6 and O = nibbles 1,3,5,7, each moved to the
+    // nibble position of its byte that the magic expects (bits 0-3 for bf16,
+    // 4-7 for fp16)
+    const uint32_t s_lo = F16A ? 4u : 0u, s_hi = F16A ? 0u : 4u;
+    sh_e = high ? s_hi : s_lo;
+    sh_o = high ? s_lo : s_hi;
+    asm volatile("" : "+v"(mask_e), "+s"(magic4), "+s"(sel_a), "+s"(sel_b), "+s"(sh_e), "+s"(sh_o));
+  }
+  __device__ __forceinline__ uint32_t shifted(uint32_t w, uint32_t sh, bool lo_role) const {
+    // bf16: bits 0-3 <- (w >> sh); fp16: bits 4-7 <- (w << sh)
+    return F16A ? (w << sh) : (w >> sh);
+  }
+  __device__ __forceinline__ i32x4 operator()(uint32_t w) const {
+    uint32_t e, o;
+    if constexpr (UINT4) {  // low order known at compile time
+      e = F16A ? (w << 4) & mask_e : w & mask_e;
+      o = F16A ? w & mask_e : (w >> 4) & mask_e;
+    } else {
+      e = shifted(w, sh_e, true) & mask_e;
+      o = shifted(w, sh_o, false) & mask_e;
+    }
+    i32x4 r;
+    r[0] = static_cast<int>(__builtin_amdgcn_perm(magic4, e, sel_a));
+    r[1] = static_cast<int>(__builtin_amdgcn_perm(magic4, e, sel_b));
+    r[2] = static_cast<int>(__builtin_amdgcn_perm(magic4, o, sel_a));
+    r[3] = static_cast<int>(__builtin_amdgcn_perm(magic4, o, sel_b));
+    return r;
+  }
+};
+
+// 8 consecutive 16-bit activations (4 registers) -> order (0 2 4 6 1 3 5 7).
+__device__ __forceinline__ i32x4 even_odd(const i32x4& v) {
+  i32x4 r;
+  r[0] = static_cast<int>(__builtin_amdgcn_perm(v[1], v[0], 0x05040100u));
+  r[1] = static_cast<int>(__builtin_amdgcn_perm(v[3], v[2], 0x05040100u));
+  r[2] = static_cast<int>(__builtin_amdgcn_perm(v[1], v[0], 0x07060302u));
+  r[3] = static_cast<int>(__builtin_amdgcn_perm(v[3], v[2], 0x07060302u));
+  return r;
+}
+
+template <int CT, int SPC, bool UINT4>
+struct DecodeChunk {
+  uint32_t w[CT][4];
+  GroupRaw gr[CT][UINT4 ? 1 : SPC];  // UINT4: scales / zero points come in one batch
+};
+
+// RP: activation rows held per slab (1, 4 or 16; rows past M repeat row M-1).
+template <int RP, int CT, int G, bool KN, bool F16A, int WAVES, bool UINT4>
+__global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
+#pragma clang fp contract(off)
+  constexpr int SPC = 128 / G;                  // groups per chunk
+  constexpr int STEPS_PER_GROUP = 4 / SPC;
+  constexpr int CH = kDecodeChunks;
+  constexpr int ROWB = CH * 128 * 2 + 16;       // LDS bytes per activation row (padded)
+  constexpr float MAGIC = F16A ? 256.0f : 128.0f;
+  constexpr float UNIT = F16A ? 4.0f : 1.0f;
+  const uint32_t ones2 = F16A ? 0x3C003C00u : 0x3F803F80u;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 16 * CT;
+  const int m0 = blockIdx.y * RP;
+  int ncol[CT];
+  static_for<0, CT>([&](auto t) { ncol[t] = min(n0 + 16 * t + col, p.N - 1); });
+  const int C = ceil_div(p.K, 128);
+  const int KW = p.K >> 3;
+  const int cpw = ceil_div(C, WAVES);           // <= CH (checked by the launcher)
+  const int c0 = min(wave * cpw, C - 1);
+  const int nch = max(0, min(cpw, C - wave * cpw));  // chunks of this wave
+
+  Unpack7<F16A, UINT4> unpack;
+  unpack.init(!UINT4 && (p.flags & QG_W4_ORDER_HIGH));
+  // signed storage: q & 15 with q in [-8, 7] -> unsigned u = q + 8 = nibble ^ 8
+  const uint32_t wxor = (!UINT4 && (p.flags & QG_W4_SIGNED_NIBBLES)) ? 0x88888888u : 0u;
+  const i32x4 ones = {static_cast<int>(ones2), static_cast<int>(ones2), static_cast<int>(ones2),
+                      static_cast<int>(ones2)};
+  auto woff = [&](int n, int kw) -> uint32_t {
+    return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (static_cast<uint32_t>(n) * KW + kw);
+  };
+
+  // ---- 1. this wave's activation slice (issued first: it is needed first) --
+  i32x4 av[RP];
+  {
+    const int k = min(c0 * 128 + 8 * lane, p.K - 8);
+    static_for<0, RP>([&](auto r) {
+      const uint32_t roff = 2u * static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.a_sm);
+      av[r] = load_at<i32x4>(p.a, roff + 2u * k);
+    });
+  }
+
+  // ---- 2. every weight / scale / zero load of this wave, in chunk order ----
+  // UINT4 (group 128: one group per chunk): the wave's <= 4 groups lie in one
+  // aligned run of 8 (launcher: ng % 8 == 0, chunks per wave divide 8), so one
+  // 16-byte load holds their bf16 scales and one word their zero points.
+  i32x4 s8[CT];
+  uint32_t z8[CT];
+  if constexpr (UINT4) {
+    const int g8 = c0 & ~7;
+    static_for<0, CT>([&](auto t) {
+      s8[t] = load_at<i32x4>(p.scales, 2u * (static_cast<uint32_t>(ncol[t]) * p.ng + g8));
+      z8[t] = load_at<uint32_t>(p.zeros, 4u * (static_cast<uint32_t>(ncol[t]) * p.zw + (g8 >> 3)));
+    });
+  }
+  DecodeChunk<CT, SPC, UINT4> ch[CH];
+  static_for<0, CH>([&](auto cl) {
+    const int c = min(c0 + cl, C - 1);
+    const int kw0 = c * 16;
+    static_for<0, CT>([&](auto t) {
+      const int n = ncol[t];
+      if constexpr (!KN && G == 128) {
+        const i32x4 v = load_at<i32x4>(p.w, woff(n, kw0 + 4 * q));
+        static_for<0, 4>([&](auto j) { ch[cl].w[t][j] = static_cast<uint32_t>(v[int(j)]); });
+      } else if constexpr (!KN && G == 64) {
+        const uint2 v0 = load_at<uint2>(p.w, woff(n, kw0 + 2 * q));
+        const uint2 v1 = load_at<uint2>(p.w, woff(n, min(kw0 + 8 + 2 * q, KW - 2)));
+        ch[cl].w[t][0] = v0.x;
+        ch[cl].w[t][1] = v0.y;
+        ch[cl].w[t][2] = v1.x;
+        ch[cl].w[t][3] = v1.y;
+      } else {
+        static_for<0, 4>([&](auto j) {
+          ch[cl].w[t][j] = load_at<uint32_t>(p.w, woff(n, min(kw0 + word_of<G, KN>(q, j), KW - 1)));
+        });
+      }
+      if constexpr (!UINT4)
+        static_for<0, SPC>([&](auto g) { ch[cl].gr[t][g] = load_group(p, n, min(c * SPC + g, p.ng - 1)); });
+    });
+  });
+
+  // keep every load above this point: the scheduler would otherwise sink
+  // them next to their first use to save registers and serialise the latency
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 3. activations -> this wave's LDS rows, even/odd order --------------
+  char* const abase = smem + wave * RP * ROWB;
+  static_for<0, RP>([&](auto r) { *reinterpret_cast<i32x4*>(abase + r * ROWB + 16 * lane) = even_odd(av[r]); });
+
+  f32x4 total[CT], acc[CT], asum;
+  static_for<0, CT>([&](auto t) { total[t] = f32x4{0, 0, 0, 0}; });
+  const char* const arow = abase + min(col, RP - 1) * ROWB;
+
+  // ---- 4. chunks in order, each as soon as its loads have landed -----------
+  static_for<0, CH>([&](auto cl) {
+    const int c = c0 + cl;
+    const bool live = cl < nch;
+    static_for<0, 4>([&](auto j) {
+      if constexpr (j % STEPS_PER_GROUP == 0) {
+        asum = f32x4{0, 0, 0, 0};
+        static_for<0, CT>([&](auto t) { acc[t] = f32x4{0, 0, 0, 0}; });
+      }
+      const i32x4 af = *reinterpret_cast<const i32x4*>(arow + 2 * (cl * 128 + 8 * word_of<G, KN>(q, j)));
+      asum = mfma16<F16A>(af, ones, asum);
+      static_for<0, CT>([&](auto t) {
+        acc[t] = mfma16<F16A>(af, unpack(UINT4 ? ch[cl].w[t][j] : ch[cl].w[t][j] ^ wxor), acc[t]);
+      });
+      if constexpr (j % STEPS_PER_GROUP == STEPS_PER_GROUP - 1) {
+        constexpr int gi = j / STEPS_PER_GROUP;
+        static_for<0, CT>([&](auto t) {
+          GroupParams gp;
+          if constexpr (UINT4) {
+            // group within the aligned run of 8 (c == g); past the run only for
+            // chunks that are not live (their scale is zeroed below)
+            const int gl = min((c0 & 7) + cl, 7);
+            const int h = gl >> 1;
+            const uint32_t sw = static_cast<uint32_t>(
+                (h & 2) ? ((h & 1) ? s8[t][3] : s8[t][2]) : ((h & 1) ? s8[t][1] : s8[t][0]));
+            gp.s = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16)) / UNIT;
+            gp.zb = MAGIC + UNIT * static_cast<float>((z8[t] >> (4 * gl)) & 15u);
+          } else {
+            gp = decode_group<false>(p, ch[cl].gr[t][gi], ncol[t], c * SPC + gi, MAGIC, UNIT);
+          }
+          if (!live || c * SPC + gi >= p.ng) gp.s = 0.0f;
+          static_for<0, 4>([&](auto i) {
+            const float v = __builtin_fmaf(-gp.zb, asum[int(i)], acc[t][int(i)]);
+            total[t][int(i)] = __builtin_fmaf(gp.s, v, total[t][int(i)]);
+          });
+        });
+      }
+    });
+  });
+
+  // ---- 5. fixed-order reduction of the WAVES partial tiles -----------------
+  __syncthreads();  // every wave is done with its activation slice
+  float* red = reinterpret_cast<float*>(smem);  // [WAVES][16][16*CT + 1]
+  constexpr int RS = 16 * CT + 1;
+  static_for<0, CT>([&](auto t) {
+    static_for<0, 4>([&](auto i) { red[(wave * 16 + 4 * q + i) * RS + 16 * t + col] = total[t][int(i)]; });
+  });
+  __syncthreads();
+  for (int e = threadIdx.x; e < RP * 16 * CT; e += 64 * WAVES) {
+    const int r = e / (16 * CT), cc = e % (16 * CT);
+    const int row = m0 + r, nn = n0 + cc;
+    if (row < p.M && nn < p.N) {
+      float v = red[r * RS + cc];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) v = v + red[(w * 16 + r) * RS + cc];
+      if (p.bias) v = v + load_bias(p.bias, p.bias_dtype, nn);
+      store_out(p.out, p.out_dtype, static_cast<int64_t>(row) * p.N + nn, v);
+    }
+  }
+}
+
+// --------------------------------------------------------------- GEMV kernel
+// M <= 4: a streaming matrix-vector kernel. Each wave owns one 16-column tile
+// and a contiguous range of 128-wide K chunks (the whole K when N alone fills
+// the GPU, else K is split KS ways and the KS partial tiles of a column tile
+// are summed through LDS in a fixed order). The workgroup first stages its
+// RP activation rows, whole K, in LDS (even/odd order, as the decode kernel)
+// together with the per-row sums of every quantisation group, so the waves
+// need neither activation loads nor an MFMA against ones. A wave then streams
+// its weight words with a rolling window of GDEPTH chunks in flight: chunk c
+// is computed as soon as it lands and its slot is refilled with chunk
+// c + GDEPTH, so compute overlaps the memory stream instead of following it.
+constexpr int kGemvDepth = 8;
+
+template <int SPC>
+struct GemvChunk {
+  uint32_t w[4];
+  GroupRaw gr[SPC];
+};
+
+template <int RP, int KS, int G, bool KN, bool F16A, bool UINT4>
+__global__ __launch_bounds__(256) void k_w4_gemv(W4Args p) {
+#pragma clang fp contract(off)
+  constexpr int SPC = 128 / G;
+  constexpr int STEPS_PER_GROUP = 4 / SPC;
+  constexpr int TPB = 4 / KS;                   // column tiles per workgroup
+  constexpr int D = kGemvDepth;
+  constexpr float MAGIC = F16A ? 256.0f : 128.0f;
+  constexpr float UNIT = F16A ? 4.0f : 1.0f;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, q = lane >> 4;
+  const int tile = wave % TPB, part = wave / TPB;
+  const int n0 = (blockIdx.x * TPB + tile) * 16;
+  const int n = min(n0 + col, p.N - 1);
+  const int m0 = blockIdx.y * RP;
+  const int R = min(p.M - m0, RP);
+  const int C = ceil_div(p.K, 128);
+  const int KW = p.K >> 3;
+  const int KP = C * 128;                       // padded K of the staged rows
+  const int ROWB = 2 * KP + 16;                 // LDS bytes per staged row
+  char* const a_lds = smem;                     // [RP][ROWB]
+  float* const asum_lds = reinterpret_cast<float*>(smem + RP * ROWB);  // [ng][4]
+
+  // ---- 1. this part's weight / scale / zero loads start first -------------
+  const int cb = part * C / KS, ce = (part + 1) * C / KS;  // chunk range [cb, ce)
+  const int clast = max(cb, ce - 1);
+  auto woff = [&](int kw) -> uint32_t {
+    return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (static_cast<uint32_t>(n) * KW + kw);
+  };
+  auto load = [&](GemvChunk<SPC>& ch, int c) {
+    const int kw0 = c * 16;
+    if constexpr (!KN && G == 128) {
+      const i32x4 v = load_at<i32x4>(p.w, woff(kw0 + 4 * q));
+      static_for<0, 4>([&](auto j) { ch.w[j] = static_cast<uint32_t>(v[int(j)]); });
+    } else if constexpr (!KN && G == 64) {
+      const uint2 v0 = load_at<uint2>(p.w, woff(kw0 + 2 * q));
+      const uint2 v1 = load_at<uint2>(p.w, woff(min(kw0 + 8 + 2 * q, KW - 2)));
+      ch.w[0] = v0.x;
+      ch.w[1] = v0.y;
+      ch.w[2] = v1.x;
+      ch.w[3] = v1.y;
+    } else {
+      static_for<0, 4>([&](auto j) {
+        ch.w[j] = load_at<uint32_t>(p.w, woff(min(kw0 + word_of<G, KN>(q, j), KW - 1)));
+      });
+    }
+    static_for<0, SPC>([&](auto g) { ch.gr[g] = load_group(p, n, min(c * SPC + g, p.ng - 1)); });
+  };
+  GemvChunk<SPC> buf[D];
+  static_for<0, D>([&](auto d) { load(buf[d], min(cb + d, clast)); });
+
+  // ---- 2. stage the activation rows (whole K) and their group sums --------
+  for (int e = threadIdx.x; e < RP * (KP / 8); e += 256) {
+    const int r = e / (KP / 8), k = 8 * (e % (KP / 8));
+    const uint32_t roff = 2u * static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.a_sm);
+    i32x4 v = load_at<i32x4>(p.a, roff + 2u * min(k, p.K - 8));
+    if (k >= p.K) v = i32x4{0, 0, 0, 0};        // K padding to whole chunks
+    *reinterpret_cast<i32x4*>(a_lds + r * ROWB + 2 * k) = even_odd(v);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < p.ng * 4; e += 256) {
+    const int g = e >> 2, r = e & 3;
+    float sum = 0.0f;
+    if (r < RP) {
+      const char* src = a_lds + r * ROWB + 2 * g * p.group;
+      for (int k = 0; k < p.group; k += 8) {
+        const i32x4 v = *reinterpret_cast<const i32x4*>(src + 2 * k);
+        static_for<0, 4>([&](auto h) {
+          const uint32_t u = static_cast<uint32_t>(v[int(h)]);
+          const float lo = F16A ? f16_to_f32(static_cast<uint16_t>(u)) : bf16_to_f32(static_cast<uint16_t>(u));
+          const float hi = F16A ? f16_to_f32(static_cast<uint16_t>(u >> 16)) : bf16_to_f32(static_cast<uint16_t>(u >> 16));
+          sum = sum + lo;
+          sum = sum + hi;
+        });
+      }
+    }
+    asum_lds[e] = sum;
+  }
+  __syncthreads();
+
+  // ---- 3. stream the chunks -------------------------------------------------
+  Unpack7<F16A, UINT4> unpack;
+  unpack.init(!UINT4 && (p.flags & QG_W4_ORDER_HIGH));
+  const uint32_t wxor = (!UINT4 && (p.flags & QG_W4_SIGNED_NIBBLES)) ? 0x88888888u : 0u;
+  const char* const arow = a_lds + min(col, R - 1) * ROWB;
+  // accumulator rows 4q..4q+3 are real rows only for q == 0 (RP <= 4); the
+  // other lanes use the same group sums and produce rows that are not stored
+  constexpr int srow = 0;
+  f32x4 total = {0, 0, 0, 0}, acc;
+  auto compute = [&](const GemvChunk<SPC>& ch, int c, bool live) {
+    static_for<0, 4>([&](auto j) {
+      const i32x4 af = *reinterpret_cast<const i32x4*>(arow + 2 * (c * 128 + 8 * word_of<G, KN>(q, j)));
+      const i32x4 b = unpack(UINT4 ? ch.w[j] : ch.w[j] ^ wxor);
+      if constexpr (j % STEPS_PER_GROUP == 0) acc = mfma16<F16A>(af, b, f32x4{0, 0, 0, 0});
+      else acc = mfma16<F16A>(af, b, acc);
+      if constexpr (j % STEPS_PER_GROUP == STEPS_PER_GROUP - 1) {
+        constexpr int gi = j / STEPS_PER_GROUP;
+        const int g = c * SPC + gi;
+        GroupParams gp = decode_group<UINT4>(p, ch.gr[gi], n, g, MAGIC, UNIT);
+        if (!live || g >= p.ng) gp.s = 0.0f;
+        const f32x4 as = *reinterpret_cast<const f32x4*>(asum_lds + 4 * min(g, p.ng - 1) + srow);
+        static_for<0, 4>([&](auto i) {
+          const float v = __builtin_fmaf(-gp.zb, as[int(i)], acc[int(i)]);
+          total[int(i)] = __builtin_fmaf(gp.s, v, total[int(i)]);
+        });
+      }
+    });
+  };
+  for (int base = cb; base <= clast; base += D) {
+    static_for<0, D>([&](auto d) {
+      const int c = base + d;
+      compute(buf[d], min(c, clast), c < ce);  // a part may own no chunk (C < KS)
+      load(buf[d], min(c + D, clast));
+    });
+  }
+
+  // ---- 4. results: rows 4q + i of column n0 + col ---------------------------
+  if constexpr (KS == 1) {
+    static_for<0, 4>([&](auto i) {
+      const int row = m0 + 4 * q + i;
+      if (4 * q + i < R && n0 + col < p.N) {
+        float v = total[int(i)];
+        if (p.bias) v = v + load_bias(p.bias, p.bias_dtype, n0 + col);
+        store_out(p.out, p.out_dtype, static_cast<int64_t>(row) * p.N + n0 + col, v);
+      }
+    });
+  } else {
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);  // [4 waves][4 rows][16 cols]
+    if (q == 0) static_for<0, 4>([&](auto i) { red[(wave * 4 + i) * 16 + col] = total[int(i)]; });
+    __syncthreads();
+    for (int e = threadIdx.x; e < TPB * 4 * 16; e += 256) {
+      const int t = e / 64, i = (e / 16) & 3, cc = e & 15;
+      const int nn = (blockIdx.x * TPB + t) * 16 + cc;
+      if (i < R && nn < p.N) {
+        float v = red[(t * 4 + i) * 16 + cc];
+#pragma unroll
+        for (int pp = 1; pp < KS; ++pp) v = v + red[((pp * TPB + t) * 4 + i) * 16 + cc];
+        if (p.bias) v = v + load_bias(p.bias, p.bias_dtype, nn);
+        store_out(p.out, p.out_dtype, static_cast<int64_t>(m0 + i) * p.N + nn, v);
+      }
     }
   }
 }
@@ -372,29 +837,131 @@ __global__ void k_w4_unpack(W4Args p) {
   }
 }
 
-template <int FM, int G, bool KN, bool F16A>
+template <int FM, int CT, int G, bool KN, bool F16A>
 hipError_t launch_skinny_t(const W4Args& p, hipStream_t stream) {
-  constexpr int DEPTH = FM == 1 ? 4 : 2;
-  dim3 grid(ceil_div(p.N, 16), ceil_div(p.M, 16 * FM));
-  hipLaunchKernelGGL((k_w4_skinny<FM, G, KN, F16A, DEPTH>), grid, dim3(256), 0, stream, p);
+  constexpr int DEPTH = (FM * CT <= 2) ? 4 : 2;
+  constexpr int WAVES = 8;
+  dim3 grid(ceil_div(p.N, 16 * CT), ceil_div(p.M, 16 * FM));
+  constexpr int kUint4Flags = QG_W4_ZEROS_PACKED;
+  if (G == 128 && !KN && !p.scale_f32 && p.flags == kUint4Flags)
+    hipLaunchKernelGGL((k_w4_skinny<FM, CT, G, KN, F16A, DEPTH, WAVES, (G == 128 && !KN)>), grid,
+                       dim3(64 * WAVES), 0, stream, p);
+  else
+    hipLaunchKernelGGL((k_w4_skinny<FM, CT, G, KN, F16A, DEPTH, WAVES, false>), grid, dim3(64 * WAVES), 0,
+                       stream, p);
   return hipGetLastError();
 }
 
-template <int FM, bool F16A>
+template <int FM, int CT, bool F16A>
 hipError_t launch_skinny_g(const W4Args& p, hipStream_t stream) {
   const bool kn = p.flags & QG_W4_LAYOUT_KN;
   switch (p.group) {
-    case 128: return kn ? launch_skinny_t<FM, 128, true, F16A>(p, stream) : launch_skinny_t<FM, 128, false, F16A>(p, stream);
-    case 64: return kn ? launch_skinny_t<FM, 64, true, F16A>(p, stream) : launch_skinny_t<FM, 64, false, F16A>(p, stream);
-    default: return kn ? launch_skinny_t<FM, 32, true, F16A>(p, stream) : launch_skinny_t<FM, 32, false, F16A>(p, stream);
+    case 128: return kn ? launch_skinny_t<FM, CT, 128, true, F16A>(p, stream) : launch_skinny_t<FM, CT, 128, false, F16A>(p, stream);
+    case 64: return kn ? launch_skinny_t<FM, CT, 64, true, F16A>(p, stream) : launch_skinny_t<FM, CT, 64, false, F16A>(p, stream);
+    default: return kn ? launch_skinny_t<FM, CT, 32, true, F16A>(p, stream) : launch_skinny_t<FM, CT, 32, false, F16A>(p, stream);
   }
+}
+
+template <int RP, int CT, int G, bool KN, bool F16A, bool UINT4>
+hipError_t launch_decode_t(const W4Args& p, hipStream_t stream) {
+  constexpr int WAVES = 8;
+  const size_t a_bytes = static_cast<size_t>(WAVES) * RP * (kDecodeChunks * 256 + 16);
+  const size_t red_bytes = static_cast<size_t>(WAVES) * 16 * (16 * CT + 1) * 4;
+  const size_t lds = a_bytes > red_bytes ? a_bytes : red_bytes;
+  dim3 grid(ceil_div(p.N, 16 * CT), ceil_div(p.M, RP));
+  hipLaunchKernelGGL((k_w4_decode<RP, CT, G, KN, F16A, WAVES, UINT4>), grid, dim3(64 * WAVES), lds, stream, p);
+  return hipGetLastError();
+}
+
+template <int RP, int CT, bool F16A>
+hipError_t launch_decode_g(const W4Args& p, hipStream_t stream) {
+  const bool kn = p.flags & QG_W4_LAYOUT_KN;
+  switch (p.group) {
+    case 128: {
+      const int cpw = ceil_div(ceil_div(p.K, 128), 8);
+      if (!kn && !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED && p.ng % 8 == 0 && 8 % cpw == 0)
+        return launch_decode_t<RP, CT, 128, false, F16A, true>(p, stream);
+      return kn ? launch_decode_t<RP, CT, 128, true, F16A, false>(p, stream)
+                : launch_decode_t<RP, CT, 128, false, F16A, false>(p, stream);
+    }
+    case 64:
+      return kn ? launch_decode_t<RP, 2, 64, true, F16A, false>(p, stream)
+                : launch_decode_t<RP, 2, 64, false, F16A, false>(p, stream);
+    default:
+      return kn ? launch_decode_t<RP, 2, 32, true, F16A, false>(p, stream)
+                : launch_decode_t<RP, 2, 32, false, F16A, false>(p, stream);
+  }
+}
+
+template <int RP, int KS, int G, bool KN, bool F16A, bool UINT4>
+hipError_t launch_gemv_t(const W4Args& p, size_t lds, hipStream_t stream) {
+  constexpr int TPB = 4 / KS;
+  dim3 grid(ceil_div(p.N, 16 * TPB), ceil_div(p.M, RP));
+  hipLaunchKernelGGL((k_w4_gemv<RP, KS, G, KN, F16A, UINT4>), grid, dim3(256), lds, stream, p);
+  return hipGetLastError();
+}
+
+template <int RP, int KS, bool F16A>
+hipError_t launch_gemv_g(const W4Args& p, size_t lds, hipStream_t stream) {
+  const bool kn = p.flags & QG_W4_LAYOUT_KN;
+  switch (p.group) {
+    case 128:
+      if (!kn && !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED)
+        return launch_gemv_t<RP, KS, 128, false, F16A, true>(p, lds, stream);
+      return kn ? launch_gemv_t<RP, KS, 128, true, F16A, false>(p, lds, stream)
+                : launch_gemv_t<RP, KS, 128, false, F16A, false>(p, lds, stream);
+    case 64:
+      return kn ? launch_gemv_t<RP, KS, 64, true, F16A, false>(p, lds, stream)
+                : launch_gemv_t<RP, KS, 64, false, F16A, false>(p, lds, stream);
+    default:
+      return kn ? launch_gemv_t<RP, KS, 32, true, F16A, false>(p, lds, stream)
+                : launch_gemv_t<RP, KS, 32, false, F16A, false>(p, lds, stream);
+  }
+}
+
+// LDS bytes of the GEMV kernel: staged rows, group sums, reduction tile.
+size_t gemv_lds_bytes(int rp, const W4Args& p) {
+  const size_t kp = static_cast<size_t>(ceil_div(p.K, 128)) * 128;
+  const size_t a = rp * (2 * kp + 16) + static_cast<size_t>(p.ng) * 16;
+  return a > 1024 ? a : 1024;
 }
 
 template <bool F16A>
 hipError_t launch_skinny(const W4Args& p, hipStream_t stream) {
-  if (p.M <= 16) return launch_skinny_g<1, F16A>(p, stream);
-  if (p.M <= 32) return launch_skinny_g<2, F16A>(p, stream);
-  return launch_skinny_g<4, F16A>(p, stream);
+  const int C = ceil_div(p.K, 128);
+  const char* env_ks = getenv("QG_W4_KS");  // tuning knobs while the variants are measured
+  const char* env_path = getenv("QG_W4_PATH");
+  const int path = env_path ? atoi(env_path) : 0;  // 0 auto, 1 gemv, 2 decode, 3 skinny
+  if (path == 2 && p.M <= 16 && ceil_div(C, 8) <= kDecodeChunks)
+    return p.M == 1 ? launch_decode_g<1, 2, F16A>(p, stream) : launch_decode_g<16, 4, F16A>(p, stream);
+  if (path == 3) return launch_skinny_g<1, 4, F16A>(p, stream);
+  if (path == 1 && p.M <= 4) {
+    const int rp = p.M == 1 ? 1 : 4;
+    const size_t lds = gemv_lds_bytes(rp, p);
+    if (lds <= 64 * 1024) {
+      // split K until the column tiles times the split give ~1 wave per SIMD
+      const int tiles = ceil_div(p.N, 16);
+      int ks = tiles >= 1024 ? 1 : tiles >= 512 ? 2 : 4;
+      if (env_ks) ks = atoi(env_ks);
+      if (rp == 1)
+        return ks == 1 ? launch_gemv_g<1, 1, F16A>(p, lds, stream)
+             : ks == 2 ? launch_gemv_g<1, 2, F16A>(p, lds, stream)
+                       : launch_gemv_g<1, 4, F16A>(p, lds, stream);
+      return ks == 1 ? launch_gemv_g<4, 1, F16A>(p, lds, stream)
+           : ks == 2 ? launch_gemv_g<4, 2, F16A>(p, lds, stream)
+                     : launch_gemv_g<4, 4, F16A>(p, lds, stream);
+    }
+  }
+  if (p.M <= 16 && ceil_div(C, 8) <= kDecodeChunks) {
+    const char* env_ct = getenv("QG_W4_CT");
+    const int ct = env_ct ? atoi(env_ct) : 0;
+    if (p.M == 1) return ct == 4 ? launch_decode_g<1, 4, F16A>(p, stream) : launch_decode_g<1, 2, F16A>(p, stream);
+    if (p.M <= 4) return launch_decode_g<4, 4, F16A>(p, stream);
+    return launch_decode_g<16, 4, F16A>(p, stream);
+  }
+  if (p.M <= 16) return launch_skinny_g<1, 4, F16A>(p, stream);
+  if (p.M <= 32) return launch_skinny_g<2, 1, F16A>(p, stream);
+  return launch_skinny_g<4, 1, F16A>(p, stream);
 }
 
 }  // namespace

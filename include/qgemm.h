@@ -204,6 +204,39 @@ int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m, int64_t k
                   const void* bias, int bias_dtype, void* out, int out_dtype,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * FP8 (OCP e4m3fn / e5m2) weights.
+ * ------------------------------------------------------------------------- */
+
+/* Decode fp8 storage w [n, k] (strides w_sn, w_sk in bytes = elements) to
+ * out [n, k] contiguous in out_dtype (QG_F16 / QG_F32 / QG_BF16); exact for
+ * every finite value, 0x7f / 0xff (e4m3fn) decode to NaN, e5m2 keeps inf/NaN.
+ * Replaces: decode_fp8_weight / _decode_weight / _decode_bits
+ *   (rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:21-46, :109-124). */
+int qg_fp8_decode(const uint8_t* w, int w_dtype, int64_t w_sn, int64_t w_sk,
+                  int64_t n, int64_t k, void* out, int out_dtype, void* stream);
+
+/* FP8 weight-only linear: out[m, n] = (sum_k a[m, k] * decode(w[n, k])) *
+ * w_scale[n] + bias[n]; fp32 accumulation, scale and bias applied in fp32 in
+ * that order, one rounding to out_dtype. w_scale NULL = unscaled (the
+ * reference's storage); bias NULL or [n] of bias_dtype.
+ * Replaces: the fused path _fp8_linear of fp8_weight_gemm
+ *   (fp8_weight_gemm_v06.py:49-73, :195-206), whose products and fp32
+ *   accumulation it performs exactly; BASELINE configuration 3 adds the
+ *   per-channel scale (s = absmax / 448).
+ * a: [m, k] QG_F16 / QG_BF16 with strides (a_sm, a_sk); w: [n, k] with strides
+ * (w_sn, w_sk); out: [m, n] contiguous QG_F16 / QG_BF16 / QG_F32. Operands that
+ * are not canonical (unit K stride, 16-byte aligned rows, k % 128 == 0) are
+ * packed, zero-padded, into the workspace (qg_fp8w_gemm_workspace_bytes). */
+size_t qg_fp8w_gemm_workspace_bytes(const void* a, int64_t a_sm, int64_t a_sk,
+                                    const uint8_t* w, int64_t w_sn, int64_t w_sk,
+                                    int64_t m, int64_t n, int64_t k);
+int qg_fp8w_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_sk, int64_t m,
+                 int64_t k, const uint8_t* w, int w_dtype, int64_t w_sn,
+                 int64_t w_sk, int64_t n, const float* w_scale, const void* bias,
+                 int bias_dtype, void* out, int out_dtype, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

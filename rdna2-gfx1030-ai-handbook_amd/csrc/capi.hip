@@ -247,6 +247,8 @@ extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t 
 namespace {
 
 constexpr int kW4Flags = QG_W4_SIGNED_NIBBLES | QG_W4_ORDER_HIGH | QG_W4_LAYOUT_KN | QG_W4_ZEROS_PACKED;
+// Above this many rows the W4A16 GEMM uses the tiled kernel.
+constexpr int64_t kW4TiledMinRows = 64;
 
 // int4_weight_gemm_v07.py:436-440: group 32/64/128 dividing K, nonempty, N*K < 2^31.
 bool valid_w4_shape(int64_t n, int64_t k, int group, int flags) {
@@ -354,5 +356,128 @@ extern "C" int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m
   p.bias_dtype = bias_dtype;
   p.out = out;
   p.out_dtype = out_dtype;
+  // large M: the tiled kernel (activation rows staged in LDS, 128-wide K stages)
+  if (m > kW4TiledMinRows && k % 128 == 0) {
+    qg::WdArgs t{};
+    t.a = p.a;
+    t.a_sm = p.a_sm;
+    t.a_f16 = p.a_f16;
+    t.M = p.M;
+    t.N = p.N;
+    t.K = p.K;
+    t.w4 = p.w;
+    t.flags = p.flags;
+    t.group = p.group;
+    t.ng = p.ng;
+    t.zw = p.zw;
+    t.scales = p.scales;
+    t.scale_f32 = p.scale_f32;
+    t.zeros = p.zeros;
+    t.bias = bias;
+    t.bias_dtype = bias_dtype;
+    t.out = out;
+    t.out_dtype = out_dtype;
+    return qg::launch_wd_w4(t, static_cast<hipStream_t>(stream));
+  }
   return qg::launch_w4a16(p, static_cast<hipStream_t>(stream));
+}
+
+// --------------------------------------------------------------------------
+// FP8 weights.
+namespace {
+
+bool fp8_dtype(int d) { return d == QG_E4M3 || d == QG_E5M2; }
+
+// Operands of the tiled kernel: unit K stride, 16-byte aligned rows, K a
+// multiple of the 128-wide stage; anything else is packed into workspace.
+struct Fp8Plan {
+  bool pack_a, pack_w;
+  int64_t kp;
+  size_t a_bytes, w_bytes;
+  size_t total() const { return a_bytes + w_bytes; }
+};
+
+Fp8Plan plan_fp8(const void* a, int64_t a_sm, int64_t a_sk, const void* w, int64_t w_sn, int64_t w_sk,
+                 int64_t m, int64_t n, int64_t k) {
+  Fp8Plan pl;
+  pl.kp = round_up(k, kStageK);
+  pl.pack_a = !(a_sk == 1 && a_sm % 8 == 0 && aligned16(a) && k % kStageK == 0);
+  pl.pack_w = !(w_sk == 1 && w_sn % 16 == 0 && aligned16(w) && k % kStageK == 0);
+  pl.a_bytes = pl.pack_a ? static_cast<size_t>(round_up(2 * m * pl.kp, 256)) : 0;
+  pl.w_bytes = pl.pack_w ? static_cast<size_t>(round_up(n * pl.kp, 256)) : 0;
+  return pl;
+}
+
+bool valid_fp8_shape(int64_t m, int64_t n, int64_t k, int64_t a_sm, int64_t a_sk, int64_t w_sn, int64_t w_sk) {
+  if (m < 0 || n < 0 || k < 0 || m > kIntMax || n > kIntMax || k > kIntMax) return false;
+  if (a_sm < 0 || a_sk < 0 || w_sn < 0 || w_sk < 0) return false;
+  return m * n < (int64_t(1) << 40);
+}
+
+}  // namespace
+
+extern "C" int qg_fp8_decode(const uint8_t* w, int w_dtype, int64_t w_sn, int64_t w_sk, int64_t n, int64_t k,
+                             void* out, int out_dtype, void* stream) {
+  if (!fp8_dtype(w_dtype) || !float_dtype(out_dtype)) return hipErrorInvalidValue;
+  if (n < 0 || k < 0 || w_sn < 0 || w_sk < 0 || n * k >= (int64_t(1) << 40)) return hipErrorInvalidValue;
+  if (n == 0 || k == 0) return hipSuccess;
+  if (!w || !out) return hipErrorInvalidValue;
+  return qg::launch_fp8_decode(w, w_sn, w_sk, n, k, w_dtype == QG_E5M2, out, out_dtype,
+                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t qg_fp8w_gemm_workspace_bytes(const void* a, int64_t a_sm, int64_t a_sk, const uint8_t* w,
+                                               int64_t w_sn, int64_t w_sk, int64_t m, int64_t n, int64_t k) {
+  if (!valid_fp8_shape(m, n, k, a_sm, a_sk, w_sn, w_sk)) return 0;
+  return plan_fp8(a, a_sm, a_sk, w, w_sn, w_sk, m, n, k).total();
+}
+
+extern "C" int qg_fp8w_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_sk, int64_t m, int64_t k,
+                            const uint8_t* w, int w_dtype, int64_t w_sn, int64_t w_sk, int64_t n,
+                            const float* w_scale, const void* bias, int bias_dtype, void* out, int out_dtype,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (!valid_fp8_shape(m, n, k, a_sm, a_sk, w_sn, w_sk)) return hipErrorInvalidValue;
+  if ((a_dtype != QG_F16 && a_dtype != QG_BF16) || !fp8_dtype(w_dtype)) return hipErrorInvalidValue;
+  if (!float_dtype(out_dtype) || (bias && !float_dtype(bias_dtype))) return hipErrorInvalidValue;
+  if (m == 0 || n == 0) return hipSuccess;
+  if (!out || (k > 0 && (!a || !w))) return hipErrorInvalidValue;
+  const Fp8Plan pl = plan_fp8(a, a_sm, a_sk, w, w_sn, w_sk, m, n, k);
+  if (pl.total() > 0 && (!workspace || workspace_bytes < pl.total() || !aligned16(workspace)))
+    return hipErrorInvalidValue;
+  // 32-bit byte offsets inside the kernel
+  if (2 * m * pl.kp >= kMaxOperandBytes * 2 || n * pl.kp >= kMaxOperandBytes) return hipErrorInvalidValue;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  qg::WdArgs p{};
+  p.M = static_cast<int>(m);
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(pl.kp);
+  p.a_f16 = a_dtype == QG_F16;
+  if (pl.pack_a) {
+    uint16_t* pa = reinterpret_cast<uint16_t*>(ws);
+    hipError_t e = qg::launch_pack_rows_u16(static_cast<const uint16_t*>(a), a_sm, a_sk, m, k, pa, pl.kp, s);
+    if (e != hipSuccess) return e;
+    p.a = pa;
+    p.a_sm = pl.kp;
+  } else {
+    p.a = static_cast<const uint16_t*>(a);
+    p.a_sm = a_sm;
+  }
+  if (pl.pack_w) {
+    int8_t* pw = reinterpret_cast<int8_t*>(ws + pl.a_bytes);
+    hipError_t e = qg::launch_pack_rows_i8(reinterpret_cast<const int8_t*>(w), w_sn, w_sk, n, k, pw, pl.kp, s);
+    if (e != hipSuccess) return e;
+    p.w8 = reinterpret_cast<const uint8_t*>(pw);
+    p.w8_sn = pl.kp;
+  } else {
+    p.w8 = w;
+    p.w8_sn = w_sn;
+  }
+  p.fp8_e5 = w_dtype == QG_E5M2;
+  p.w_scale = w_scale;
+  p.bias = bias;
+  p.bias_dtype = bias_dtype;
+  p.out = out;
+  p.out_dtype = out_dtype;
+  return qg::launch_wd_fp8(p, s);  // k == 0: no stage, out = bias (or 0)
 }

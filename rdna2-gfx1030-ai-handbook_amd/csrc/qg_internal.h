@@ -69,6 +69,37 @@ struct W4PackArgs {
   int32_t* sums;         // nullptr or [N, K/G]
 };
 
+// Tiled weight-decode GEMM (M large): A [M, K] fp16 / bf16 (unit K stride,
+// 16-byte aligned rows, K % 128 == 0) times INT4 or fp8 weights.
+struct WdArgs {
+  const uint16_t* a;
+  int64_t a_sm;
+  int a_f16;
+  int M, N, K;
+  // INT4 weights (same storage fields as W4Args)
+  const uint32_t* w4;
+  int flags, group, ng, zw;
+  const void* scales;
+  int scale_f32;
+  const void* zeros;
+  // fp8 weights [N, K] with row stride w8_sn (bytes, multiple of 16)
+  const uint8_t* w8;
+  int64_t w8_sn;
+  int fp8_e5;
+  const float* w_scale;  // nullptr or per-channel [N]
+  const void* bias;
+  int bias_dtype;
+  void* out;  // [M, N] contiguous
+  int out_dtype;
+};
+
+hipError_t launch_wd_w4(const WdArgs& p, hipStream_t stream);
+hipError_t launch_pack_rows_u16(const uint16_t* src, int64_t s_r, int64_t s_k, int64_t rows, int64_t K,
+                                uint16_t* dst, int64_t k_pad, hipStream_t stream);
+hipError_t launch_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64_t n, int64_t K, int e5,
+                             void* out, int out_dtype, hipStream_t stream);
+hipError_t launch_wd_fp8(const WdArgs& p, hipStream_t stream);
+
 hipError_t launch_w4a16(const W4Args& p, hipStream_t stream);
 hipError_t launch_w4_pack(const W4PackArgs& p, hipStream_t stream);
 hipError_t launch_w4_unpack(const W4Args& p, hipStream_t stream);

@@ -462,16 +462,17 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
   }
 
   // ---- 2. every weight / scale / zero load of this wave, in chunk order ----
-  // UINT4 (group 128: one group per chunk): the wave's <= 4 groups lie in one
-  // aligned run of 8 (launcher: ng % 8 == 0, chunks per wave divide 8), so one
-  // 16-byte load holds their bf16 scales and one word their zero points.
-  i32x4 s8[CT];
+  // UINT4 (group 128: chunk c is group c; launcher: 4 chunks per wave and
+  // ng % 4 == 0): the wave's 4 groups start at a multiple of 4, so one 8-byte
+  // load holds their bf16 scales and one word their zero points (nibbles
+  // 4 * (g0 % 8) + 4 cl). Waves past K read an aligned in-range quad.
+  uint2 s4[CT];
   uint32_t z8[CT];
+  const int g0 = min(c0, (p.ng - 1) & ~3);
   if constexpr (UINT4) {
-    const int g8 = c0 & ~7;
     static_for<0, CT>([&](auto t) {
-      s8[t] = load_at<i32x4>(p.scales, 2u * (static_cast<uint32_t>(ncol[t]) * p.ng + g8));
-      z8[t] = load_at<uint32_t>(p.zeros, 4u * (static_cast<uint32_t>(ncol[t]) * p.zw + (g8 >> 3)));
+      s4[t] = load_at<uint2>(p.scales, 2u * (static_cast<uint32_t>(ncol[t]) * p.ng + g0));
+      z8[t] = load_at<uint32_t>(p.zeros, 4u * (static_cast<uint32_t>(ncol[t]) * p.zw + (g0 >> 3)));
     });
   }
   DecodeChunk<CT, SPC, UINT4> ch[CH];
@@ -511,6 +512,23 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
   f32x4 total[CT], acc[CT], asum;
   static_for<0, CT>([&](auto t) { total[t] = f32x4{0, 0, 0, 0}; });
   const char* const arow = abase + min(col, RP - 1) * ROWB;
+  // accumulator registers that hold real rows: all 4 for RP >= 4, only
+  // register 0 (row 0, lanes 0-15) for a single activation row
+  constexpr int NI = RP == 1 ? 1 : 4;
+
+  // UINT4: decode the wave's group scales / zero points once
+  float gs[CT][CH], gz[CT][CH];
+  if constexpr (UINT4) {
+    static_for<0, CT>([&](auto t) {
+      const uint32_t zs = z8[t] >> (4 * (g0 & 7));
+      static_for<0, CH>([&](auto cl) {
+        const uint32_t sw = (cl >> 1) ? s4[t].y : s4[t].x;
+        gs[t][cl] = __uint_as_float((cl & 1) ? (sw & 0xFFFF0000u) : (sw << 16)) / UNIT;
+        if (cl >= nch) gs[t][cl] = 0.0f;
+        gz[t][cl] = MAGIC + UNIT * static_cast<float>((zs >> (4 * cl)) & 15u);
+      });
+    });
+  }
 
   // ---- 4. chunks in order, each as soon as its loads have landed -----------
   static_for<0, CH>([&](auto cl) {
@@ -531,19 +549,13 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
         static_for<0, CT>([&](auto t) {
           GroupParams gp;
           if constexpr (UINT4) {
-            // group within the aligned run of 8 (c == g); past the run only for
-            // chunks that are not live (their scale is zeroed below)
-            const int gl = min((c0 & 7) + cl, 7);
-            const int h = gl >> 1;
-            const uint32_t sw = static_cast<uint32_t>(
-                (h & 2) ? ((h & 1) ? s8[t][3] : s8[t][2]) : ((h & 1) ? s8[t][1] : s8[t][0]));
-            gp.s = __uint_as_float((gl & 1) ? (sw & 0xFFFF0000u) : (sw << 16)) / UNIT;
-            gp.zb = MAGIC + UNIT * static_cast<float>((z8[t] >> (4 * gl)) & 15u);
+            gp.s = gs[t][cl];
+            gp.zb = gz[t][cl];
           } else {
             gp = decode_group<false>(p, ch[cl].gr[t][gi], ncol[t], c * SPC + gi, MAGIC, UNIT);
+            if (!live || c * SPC + gi >= p.ng) gp.s = 0.0f;
           }
-          if (!live || c * SPC + gi >= p.ng) gp.s = 0.0f;
-          static_for<0, 4>([&](auto i) {
+          static_for<0, NI>([&](auto i) {
             const float v = __builtin_fmaf(-gp.zb, asum[int(i)], acc[t][int(i)]);
             total[t][int(i)] = __builtin_fmaf(gp.s, v, total[t][int(i)]);
           });
@@ -574,169 +586,124 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
 }
 
 // --------------------------------------------------------------- GEMV kernel
-// M <= 4: a streaming matrix-vector kernel. Each wave owns one 16-column tile
-// and a contiguous range of 128-wide K chunks (the whole K when N alone fills
-// the GPU, else K is split KS ways and the KS partial tiles of a column tile
-// are summed through LDS in a fixed order). The workgroup first stages its
-// RP activation rows, whole K, in LDS (even/odd order, as the decode kernel)
-// together with the per-row sums of every quantisation group, so the waves
-// need neither activation loads nor an MFMA against ones. A wave then streams
-// its weight words with a rolling window of GDEPTH chunks in flight: chunk c
-// is computed as soon as it lands and its slot is refilled with chunk
-// c + GDEPTH, so compute overlaps the memory stream instead of following it.
-constexpr int kGemvDepth = 8;
+// M == 1, group 128, "nk" words, K <= 4096: the token-decode shape of
+// BASELINE configuration 2. One wave per workgroup and per 16-column tile,
+// over the whole K, so there is no cross-wave reduction and no barrier:
+//   1. the wave issues every load it needs at once — its activation rows
+//      (LDS staging), its columns' scales and zero points (a few 16-byte
+//      loads, 32 groups each) and all <= 32 chunks of weight words;
+//   2. it stores the activation rows to its private LDS region in even/odd
+//      order (see the decode kernel) while the weights stream in;
+//   3. it consumes the chunks in issue order, each as soon as it has landed;
+//      the per-row group sums come from an MFMA against ones;
+//   4. lanes 0-15 write their column's rows.
+// Storage formats: UINT4 (bf16 scales, packed unsigned zero points) or the
+// reference's fp32 scales + int32 zero points (signed or unsigned nibbles,
+// low or high order).
+constexpr int kGemvChunks = 32;
 
-template <int SPC>
-struct GemvChunk {
-  uint32_t w[4];
-  GroupRaw gr[SPC];
-};
-
-template <int RP, int KS, int G, bool KN, bool F16A, bool UINT4>
-__global__ __launch_bounds__(256) void k_w4_gemv(W4Args p) {
+template <int RP, bool F16A, bool UINT4>
+__global__ __launch_bounds__(64) void k_w4_gemv(W4Args p) {
 #pragma clang fp contract(off)
-  constexpr int SPC = 128 / G;
-  constexpr int STEPS_PER_GROUP = 4 / SPC;
-  constexpr int TPB = 4 / KS;                   // column tiles per workgroup
-  constexpr int D = kGemvDepth;
+  constexpr int D = kGemvChunks;
+  constexpr int ROWB = D * 128 * 2 + 16;        // LDS bytes per staged row (padded)
   constexpr float MAGIC = F16A ? 256.0f : 128.0f;
   constexpr float UNIT = F16A ? 4.0f : 1.0f;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int NI = RP == 1 ? 1 : 4;           // accumulator registers with real rows
+  constexpr int SV = UINT4 ? D / 8 : D / 4;     // 16-byte scale vectors (8 bf16 / 4 fp32)
+  constexpr int ZV = UINT4 ? 1 : D / 4;         // 16-byte zero-point vectors
+  const uint32_t ones2 = F16A ? 0x3C003C00u : 0x3F803F80u;
+  __shared__ __attribute__((aligned(16))) char a_lds[RP * ROWB];
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x;
   const int col = lane & 15, q = lane >> 4;
-  const int tile = wave % TPB, part = wave / TPB;
-  const int n0 = (blockIdx.x * TPB + tile) * 16;
+  const int n0 = blockIdx.x * 16;
   const int n = min(n0 + col, p.N - 1);
   const int m0 = blockIdx.y * RP;
   const int R = min(p.M - m0, RP);
   const int C = ceil_div(p.K, 128);
   const int KW = p.K >> 3;
-  const int KP = C * 128;                       // padded K of the staged rows
-  const int ROWB = 2 * KP + 16;                 // LDS bytes per staged row
-  char* const a_lds = smem;                     // [RP][ROWB]
-  float* const asum_lds = reinterpret_cast<float*>(smem + RP * ROWB);  // [ng][4]
 
-  // ---- 1. this part's weight / scale / zero loads start first -------------
-  const int cb = part * C / KS, ce = (part + 1) * C / KS;  // chunk range [cb, ce)
-  const int clast = max(cb, ce - 1);
-  auto woff = [&](int kw) -> uint32_t {
-    return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (static_cast<uint32_t>(n) * KW + kw);
-  };
-  auto load = [&](GemvChunk<SPC>& ch, int c) {
-    const int kw0 = c * 16;
-    if constexpr (!KN && G == 128) {
-      const i32x4 v = load_at<i32x4>(p.w, woff(kw0 + 4 * q));
-      static_for<0, 4>([&](auto j) { ch.w[j] = static_cast<uint32_t>(v[int(j)]); });
-    } else if constexpr (!KN && G == 64) {
-      const uint2 v0 = load_at<uint2>(p.w, woff(kw0 + 2 * q));
-      const uint2 v1 = load_at<uint2>(p.w, woff(min(kw0 + 8 + 2 * q, KW - 2)));
-      ch.w[0] = v0.x;
-      ch.w[1] = v0.y;
-      ch.w[2] = v1.x;
-      ch.w[3] = v1.y;
-    } else {
-      static_for<0, 4>([&](auto j) {
-        ch.w[j] = load_at<uint32_t>(p.w, woff(min(kw0 + word_of<G, KN>(q, j), KW - 1)));
-      });
-    }
-    static_for<0, SPC>([&](auto g) { ch.gr[g] = load_group(p, n, min(c * SPC + g, p.ng - 1)); });
-  };
-  GemvChunk<SPC> buf[D];
-  static_for<0, D>([&](auto d) { load(buf[d], min(cb + d, clast)); });
-
-  // ---- 2. stage the activation rows (whole K) and their group sums --------
-  for (int e = threadIdx.x; e < RP * (KP / 8); e += 256) {
-    const int r = e / (KP / 8), k = 8 * (e % (KP / 8));
+  // ---- 1. every load of the wave ------------------------------------------
+  i32x4 av[RP][D / 4];  // activation rows: lane covers K [8 lane + 512 v, +8)
+  static_for<0, RP>([&](auto r) {
     const uint32_t roff = 2u * static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.a_sm);
-    i32x4 v = load_at<i32x4>(p.a, roff + 2u * min(k, p.K - 8));
-    if (k >= p.K) v = i32x4{0, 0, 0, 0};        // K padding to whole chunks
-    *reinterpret_cast<i32x4*>(a_lds + r * ROWB + 2 * k) = even_odd(v);
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < p.ng * 4; e += 256) {
-    const int g = e >> 2, r = e & 3;
-    float sum = 0.0f;
-    if (r < RP) {
-      const char* src = a_lds + r * ROWB + 2 * g * p.group;
-      for (int k = 0; k < p.group; k += 8) {
-        const i32x4 v = *reinterpret_cast<const i32x4*>(src + 2 * k);
-        static_for<0, 4>([&](auto h) {
-          const uint32_t u = static_cast<uint32_t>(v[int(h)]);
-          const float lo = F16A ? f16_to_f32(static_cast<uint16_t>(u)) : bf16_to_f32(static_cast<uint16_t>(u));
-          const float hi = F16A ? f16_to_f32(static_cast<uint16_t>(u >> 16)) : bf16_to_f32(static_cast<uint16_t>(u >> 16));
-          sum = sum + lo;
-          sum = sum + hi;
-        });
-      }
+    static_for<0, D / 4>([&](auto v) {
+      const int k = min(512 * v + 8 * lane, p.K - 8);
+      av[r][v] = load_at<i32x4>(p.a, roff + 2u * k);
+    });
+  });
+  i32x4 sv[SV], zv[ZV];
+  static_for<0, SV>([&](auto v) {
+    const int per = UINT4 ? 8 : 4;  // groups per vector
+    const int g = min(per * v, p.ng - per);
+    sv[v] = load_at<i32x4>(p.scales, (UINT4 ? 2u : 4u) * (static_cast<uint32_t>(n) * p.ng + g));
+  });
+  static_for<0, ZV>([&](auto v) {
+    if constexpr (UINT4) {
+      zv[v] = load_at<i32x4>(p.zeros, 4u * (static_cast<uint32_t>(n) * p.zw));
+    } else {
+      const int g = min(4 * v, p.ng - 4);
+      zv[v] = load_at<i32x4>(p.zeros, 4u * (static_cast<uint32_t>(n) * p.ng + g));
     }
-    asum_lds[e] = sum;
-  }
-  __syncthreads();
+  });
+  i32x4 w[D];
+  static_for<0, D>([&](auto c) {
+    w[c] = load_at<i32x4>(p.w, 4u * (static_cast<uint32_t>(n) * KW + min(16 * c, KW - 16) + 4 * q));
+  });
+  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- 3. stream the chunks -------------------------------------------------
+  // ---- 2. activations -> LDS, even/odd order -------------------------------
+  static_for<0, RP>([&](auto r) {
+    static_for<0, D / 4>([&](auto v) {
+      *reinterpret_cast<i32x4*>(a_lds + r * ROWB + 1024 * v + 16 * lane) = even_odd(av[r][v]);
+    });
+  });
+
   Unpack7<F16A, UINT4> unpack;
   unpack.init(!UINT4 && (p.flags & QG_W4_ORDER_HIGH));
   const uint32_t wxor = (!UINT4 && (p.flags & QG_W4_SIGNED_NIBBLES)) ? 0x88888888u : 0u;
+  const i32x4 ones = {static_cast<int>(ones2), static_cast<int>(ones2), static_cast<int>(ones2),
+                      static_cast<int>(ones2)};
   const char* const arow = a_lds + min(col, R - 1) * ROWB;
-  // accumulator rows 4q..4q+3 are real rows only for q == 0 (RP <= 4); the
-  // other lanes use the same group sums and produce rows that are not stored
-  constexpr int srow = 0;
-  f32x4 total = {0, 0, 0, 0}, acc;
-  auto compute = [&](const GemvChunk<SPC>& ch, int c, bool live) {
-    static_for<0, 4>([&](auto j) {
-      const i32x4 af = *reinterpret_cast<const i32x4*>(arow + 2 * (c * 128 + 8 * word_of<G, KN>(q, j)));
-      const i32x4 b = unpack(UINT4 ? ch.w[j] : ch.w[j] ^ wxor);
-      if constexpr (j % STEPS_PER_GROUP == 0) acc = mfma16<F16A>(af, b, f32x4{0, 0, 0, 0});
-      else acc = mfma16<F16A>(af, b, acc);
-      if constexpr (j % STEPS_PER_GROUP == STEPS_PER_GROUP - 1) {
-        constexpr int gi = j / STEPS_PER_GROUP;
-        const int g = c * SPC + gi;
-        GroupParams gp = decode_group<UINT4>(p, ch.gr[gi], n, g, MAGIC, UNIT);
-        if (!live || g >= p.ng) gp.s = 0.0f;
-        const f32x4 as = *reinterpret_cast<const f32x4*>(asum_lds + 4 * min(g, p.ng - 1) + srow);
-        static_for<0, 4>([&](auto i) {
-          const float v = __builtin_fmaf(-gp.zb, as[int(i)], acc[int(i)]);
-          total[int(i)] = __builtin_fmaf(gp.s, v, total[int(i)]);
-        });
-      }
-    });
-  };
-  for (int base = cb; base <= clast; base += D) {
-    static_for<0, D>([&](auto d) {
-      const int c = base + d;
-      compute(buf[d], min(c, clast), c < ce);  // a part may own no chunk (C < KS)
-      load(buf[d], min(c + D, clast));
-    });
-  }
+  f32x4 total = {0, 0, 0, 0};
 
-  // ---- 4. results: rows 4q + i of column n0 + col ---------------------------
-  if constexpr (KS == 1) {
-    static_for<0, 4>([&](auto i) {
-      const int row = m0 + 4 * q + i;
-      if (4 * q + i < R && n0 + col < p.N) {
+  // ---- 3. chunk c = group c --------------------------------------------------
+  static_for<0, D>([&](auto c) {
+    f32x4 acc = {0, 0, 0, 0}, asum = {0, 0, 0, 0};
+    static_for<0, 4>([&](auto j) {
+      const i32x4 af = *reinterpret_cast<const i32x4*>(arow + 2 * (c * 128 + 8 * (4 * q + j)));
+      asum = mfma16<F16A>(af, ones, asum);
+      acc = mfma16<F16A>(af, unpack(UINT4 ? static_cast<uint32_t>(w[c][int(j)])
+                                          : static_cast<uint32_t>(w[c][int(j)]) ^ wxor), acc);
+    });
+    float s, zb;
+    if constexpr (UINT4) {
+      const uint32_t sw = static_cast<uint32_t>(sv[c / 8][(c % 8) / 2]);
+      s = __uint_as_float((c & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+      zb = MAGIC + UNIT * static_cast<float>((static_cast<uint32_t>(zv[0][c / 8]) >> (4 * (c % 8))) & 15u);
+    } else {
+      s = __int_as_float(sv[c / 4][c % 4]);
+      int z = zv[c / 4][c % 4];
+      if (p.flags & QG_W4_SIGNED_NIBBLES) z += 8;
+      zb = MAGIC + UNIT * static_cast<float>(z);
+    }
+    s = (c < C) ? s / UNIT : 0.0f;  // chunks past K were re-read, not counted
+    static_for<0, NI>([&](auto i) {
+      const float v = __builtin_fmaf(-zb, asum[int(i)], acc[int(i)]);
+      total[int(i)] = __builtin_fmaf(s, v, total[int(i)]);
+    });
+  });
+
+  // ---- 4. lanes 0-15: rows 0..3 of column n0 + col -------------------------
+  if (q == 0 && n0 + col < p.N) {
+    static_for<0, NI>([&](auto i) {
+      if (i < R) {
         float v = total[int(i)];
         if (p.bias) v = v + load_bias(p.bias, p.bias_dtype, n0 + col);
-        store_out(p.out, p.out_dtype, static_cast<int64_t>(row) * p.N + n0 + col, v);
+        store_out(p.out, p.out_dtype, static_cast<int64_t>(m0 + i) * p.N + n0 + col, v);
       }
     });
-  } else {
-    __syncthreads();
-    float* red = reinterpret_cast<float*>(smem);  // [4 waves][4 rows][16 cols]
-    if (q == 0) static_for<0, 4>([&](auto i) { red[(wave * 4 + i) * 16 + col] = total[int(i)]; });
-    __syncthreads();
-    for (int e = threadIdx.x; e < TPB * 4 * 16; e += 256) {
-      const int t = e / 64, i = (e / 16) & 3, cc = e & 15;
-      const int nn = (blockIdx.x * TPB + t) * 16 + cc;
-      if (i < R && nn < p.N) {
-        float v = red[(t * 4 + i) * 16 + cc];
-#pragma unroll
-        for (int pp = 1; pp < KS; ++pp) v = v + red[((pp * TPB + t) * 4 + i) * 16 + cc];
-        if (p.bias) v = v + load_bias(p.bias, p.bias_dtype, nn);
-        store_out(p.out, p.out_dtype, static_cast<int64_t>(m0 + i) * p.N + nn, v);
-      }
-    }
   }
 }
 
@@ -879,7 +846,7 @@ hipError_t launch_decode_g(const W4Args& p, hipStream_t stream) {
   switch (p.group) {
     case 128: {
       const int cpw = ceil_div(ceil_div(p.K, 128), 8);
-      if (!kn && !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED && p.ng % 8 == 0 && 8 % cpw == 0)
+      if (!kn && !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED && p.ng % 4 == 0 && cpw == kDecodeChunks)
         return launch_decode_t<RP, CT, 128, false, F16A, true>(p, stream);
       return kn ? launch_decode_t<RP, CT, 128, true, F16A, false>(p, stream)
                 : launch_decode_t<RP, CT, 128, false, F16A, false>(p, stream);
@@ -893,65 +860,33 @@ hipError_t launch_decode_g(const W4Args& p, hipStream_t stream) {
   }
 }
 
-template <int RP, int KS, int G, bool KN, bool F16A, bool UINT4>
-hipError_t launch_gemv_t(const W4Args& p, size_t lds, hipStream_t stream) {
-  constexpr int TPB = 4 / KS;
-  dim3 grid(ceil_div(p.N, 16 * TPB), ceil_div(p.M, RP));
-  hipLaunchKernelGGL((k_w4_gemv<RP, KS, G, KN, F16A, UINT4>), grid, dim3(256), lds, stream, p);
+// The GEMV kernel serves M == 1, group 128, "nk", K <= 4096 with scale /
+// zero-point rows that start on 16-byte boundaries (more activation rows do
+// not fit in registers next to the 32 chunks of weight words).
+bool gemv_fits(const W4Args& p) {
+  if (p.M != 1 || p.group != 128 || (p.flags & QG_W4_LAYOUT_KN) || p.K > kGemvChunks * 128) return false;
+  const bool uint4 = !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED;
+  const bool ref = p.scale_f32 && !(p.flags & QG_W4_ZEROS_PACKED);
+  if (uint4) return p.ng % 8 == 0 && p.zw % 4 == 0 && p.ng >= 8;
+  return ref && p.ng % 4 == 0 && p.ng >= 4;
+}
+
+template <bool F16A>
+hipError_t launch_gemv(const W4Args& p, hipStream_t stream) {
+  const bool uint4 = !p.scale_f32;
+  dim3 grid(ceil_div(p.N, 16), p.M);
+  if (uint4) hipLaunchKernelGGL((k_w4_gemv<1, F16A, true>), grid, dim3(64), 0, stream, p);
+  else hipLaunchKernelGGL((k_w4_gemv<1, F16A, false>), grid, dim3(64), 0, stream, p);
   return hipGetLastError();
-}
-
-template <int RP, int KS, bool F16A>
-hipError_t launch_gemv_g(const W4Args& p, size_t lds, hipStream_t stream) {
-  const bool kn = p.flags & QG_W4_LAYOUT_KN;
-  switch (p.group) {
-    case 128:
-      if (!kn && !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED)
-        return launch_gemv_t<RP, KS, 128, false, F16A, true>(p, lds, stream);
-      return kn ? launch_gemv_t<RP, KS, 128, true, F16A, false>(p, lds, stream)
-                : launch_gemv_t<RP, KS, 128, false, F16A, false>(p, lds, stream);
-    case 64:
-      return kn ? launch_gemv_t<RP, KS, 64, true, F16A, false>(p, lds, stream)
-                : launch_gemv_t<RP, KS, 64, false, F16A, false>(p, lds, stream);
-    default:
-      return kn ? launch_gemv_t<RP, KS, 32, true, F16A, false>(p, lds, stream)
-                : launch_gemv_t<RP, KS, 32, false, F16A, false>(p, lds, stream);
-  }
-}
-
-// LDS bytes of the GEMV kernel: staged rows, group sums, reduction tile.
-size_t gemv_lds_bytes(int rp, const W4Args& p) {
-  const size_t kp = static_cast<size_t>(ceil_div(p.K, 128)) * 128;
-  const size_t a = rp * (2 * kp + 16) + static_cast<size_t>(p.ng) * 16;
-  return a > 1024 ? a : 1024;
 }
 
 template <bool F16A>
 hipError_t launch_skinny(const W4Args& p, hipStream_t stream) {
   const int C = ceil_div(p.K, 128);
-  const char* env_ks = getenv("QG_W4_KS");  // tuning knobs while the variants are measured
-  const char* env_path = getenv("QG_W4_PATH");
-  const int path = env_path ? atoi(env_path) : 0;  // 0 auto, 1 gemv, 2 decode, 3 skinny
-  if (path == 2 && p.M <= 16 && ceil_div(C, 8) <= kDecodeChunks)
-    return p.M == 1 ? launch_decode_g<1, 2, F16A>(p, stream) : launch_decode_g<16, 4, F16A>(p, stream);
+  const char* env_path = getenv("QG_W4_PATH");  // tuning knob while the variants are measured
+  const int path = env_path ? atoi(env_path) : 0;  // 0 auto, 2 decode, 3 skinny
+  if (path == 0 && gemv_fits(p)) return launch_gemv<F16A>(p, stream);
   if (path == 3) return launch_skinny_g<1, 4, F16A>(p, stream);
-  if (path == 1 && p.M <= 4) {
-    const int rp = p.M == 1 ? 1 : 4;
-    const size_t lds = gemv_lds_bytes(rp, p);
-    if (lds <= 64 * 1024) {
-      // split K until the column tiles times the split give ~1 wave per SIMD
-      const int tiles = ceil_div(p.N, 16);
-      int ks = tiles >= 1024 ? 1 : tiles >= 512 ? 2 : 4;
-      if (env_ks) ks = atoi(env_ks);
-      if (rp == 1)
-        return ks == 1 ? launch_gemv_g<1, 1, F16A>(p, lds, stream)
-             : ks == 2 ? launch_gemv_g<1, 2, F16A>(p, lds, stream)
-                       : launch_gemv_g<1, 4, F16A>(p, lds, stream);
-      return ks == 1 ? launch_gemv_g<4, 1, F16A>(p, lds, stream)
-           : ks == 2 ? launch_gemv_g<4, 2, F16A>(p, lds, stream)
-                     : launch_gemv_g<4, 4, F16A>(p, lds, stream);
-    }
-  }
   if (p.M <= 16 && ceil_div(C, 8) <= kDecodeChunks) {
     const char* env_ct = getenv("QG_W4_CT");
     const int ct = env_ct ? atoi(env_ct) : 0;

@@ -1,0 +1,431 @@
+// Tiled weight-decode GEMM for gfx950: out = A @ dequant(W)^T (+ bias), with
+// A [M, K] fp16 / bf16 and W either INT4 groups (the W4 storage of
+// include/qgemm.h) or OCP fp8 (e4m3fn / e5m2) with an optional per-channel
+// scale. Serves the large-M shapes of int4_linear_a16
+// (rdna2-ops/rdna2_ops/int4_weight_gemm_v07.py:540-564) and fp8_weight_gemm's
+// fused path (rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:49-73, :195-206).
+//
+// Design:
+//  * one 256-thread workgroup (2 x 2 waves) per 128 x 128 output tile; each
+//    wave owns 64 x 64 as 4 x 4 fragments of v_mfma_f32_16x16x32_{bf16,f16};
+//  * K advances in 128-wide stages. The activation stage (128 rows x 256 B)
+//    is copied HBM -> LDS with global_load_lds_dwordx4 into a 2-slot ring,
+//    as two 128-byte-row halves with the 16-byte chunk index XOR-swizzled by
+//    (row & 7) — the INT8 kernel's conflict-free layout;
+//  * weights never touch LDS: each lane loads its column's words / bytes for
+//    the next stage into registers while the current stage computes, and
+//    expands them in registers right before the MFMA (nibble -> 128 + u or
+//    256 + 4u with one v_perm + one v_and_or per register; fp8 -> bf16/fp16
+//    with v_cvt_scalef32_pk_*_fp8 at scale 1, exact);
+//  * W4: each group's MFMA sum is taken separately; total += s * (acc - zb *
+//    rowsum) with the row sums from an MFMA against ones (fp32, exact
+//    products). FP8: out = acc * scale[n] + bias[n] (fp32).
+// One barrier per stage: at the top of stage s every wave waits for its own
+// copies of stage s (LDS) and its weight registers (vmcnt(0)), then the
+// workgroup barrier makes the whole stage visible and guarantees that the
+// other slot is free; stage s+1 is issued right after and overlaps stage s's
+// MFMAs.
+#include "qg_common.h"
+#include "qg_internal.h"
+
+namespace qg {
+
+namespace {
+
+constexpr int kBM = 128, kBN = 128, kKS = 128;
+constexpr int kHalf = kBM * 128;            // bytes of one 64-wide K half of a stage
+constexpr int kStage = 2 * kHalf;           // 32 KB
+constexpr int kFM = 4, kFN = 4;             // 16x16 fragments per wave
+
+enum WdFormat { WD_W4_UINT4 = 0, WD_W4_GENERIC = 1, WD_FP8_E4M3 = 2, WD_FP8_E5M2 = 3 };
+
+template <bool F16A>
+__device__ __forceinline__ f32x4 mfma16(const i32x4& a, const i32x4& b, const f32x4& c) {
+  if constexpr (F16A)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ T load_at(const void* base, uint32_t byte_off) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off);
+}
+
+// Word f (0..15) of a 128-wide stage feeds MFMA step j from lane group q; each
+// step stays inside one W4 group (same rule as the decode kernels).
+template <int G, bool KN>
+__device__ __forceinline__ int word_of(int q, int j) {
+  if constexpr (!KN && G == 128) return 4 * q + j;
+  else if constexpr (!KN && G == 64) return 8 * (j >> 1) + 2 * q + (j & 1);
+  else return 4 * j + q;
+}
+
+// Natural-order nibble expansion (register i = K elements 2i, 2i+1).
+template <bool F16A>
+__device__ __forceinline__ i32x4 unpack_nat(uint32_t w, const uint32_t (&sel)[4], uint32_t mask,
+                                            uint32_t magic2) {
+  const uint32_t lo = F16A ? w << 4 : w;
+  const uint32_t hi = F16A ? w : w >> 4;
+  i32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t t = __builtin_amdgcn_perm(hi, lo, sel[i]);
+    r[i] = static_cast<int>((t & mask) | magic2);
+  }
+  return r;
+}
+
+__device__ __forceinline__ void nat_selectors(bool high, uint32_t (&sel)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t b0 = high ? (4u + 3u - i) : static_cast<uint32_t>(i);
+    const uint32_t b2 = high ? (3u - i) : (4u + i);
+    sel[i] = 0x0C000C00u | (b2 << 16) | b0;
+  }
+}
+
+// 8 fp8 bytes (2 dwords) -> 8 bf16 / fp16 values in natural order.
+template <bool F16A, bool E5>
+__device__ __forceinline__ i32x4 fp8x8(uint32_t d0, uint32_t d1) {
+  i32x4 r;
+  if constexpr (F16A) {
+    if constexpr (E5) {
+      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d0, 1.0f, false));
+      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d0, 1.0f, true));
+      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d1, 1.0f, false));
+      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d1, 1.0f, true));
+    } else {
+      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false));
+      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true));
+      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false));
+      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true));
+    }
+  } else {
+    if constexpr (E5) {
+      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d0, 1.0f, false));
+      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d0, 1.0f, true));
+      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d1, 1.0f, false));
+      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d1, 1.0f, true));
+    } else {
+      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, false));
+      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, true));
+      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, false));
+      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, true));
+    }
+  }
+  return r;
+}
+
+__device__ __forceinline__ float bias_at(const void* bias, int dtype, int col) {
+  if (dtype == QG_F32) return static_cast<const float*>(bias)[col];
+  const uint16_t b = static_cast<const uint16_t*>(bias)[col];
+  return dtype == QG_F16 ? f16_to_f32(b) : bf16_to_f32(b);
+}
+
+__device__ __forceinline__ void put_out(void* out, int dtype, int64_t idx, float v) {
+  if (dtype == QG_F32) static_cast<float*>(out)[idx] = v;
+  else if (dtype == QG_F16) static_cast<uint16_t*>(out)[idx] = f32_to_f16(v);
+  else static_cast<uint16_t*>(out)[idx] = f32_to_bf16(v);
+}
+
+// Weight registers of one stage for one wave: FN column tiles.
+template <int FMT>
+struct StageW {
+  static constexpr int R = (FMT >= WD_FP8_E4M3) ? 8 : 4;  // 32-bit words per lane per tile
+  uint32_t w[kFN][R];
+  uint32_t gs[kFN][4], gz[kFN][4];  // W4: raw scale / zero words per group slot
+};
+
+template <int FMT, int G, bool KN, bool F16A>
+__global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
+#pragma clang fp contract(off)
+  constexpr bool W4 = FMT <= WD_W4_GENERIC;
+  constexpr bool UINT4 = FMT == WD_W4_UINT4;
+  constexpr int SPS = W4 ? kKS / G : 1;         // W4 groups per stage
+  constexpr int STEPS_PER_GROUP = 4 / SPS;
+  constexpr float MAGIC = F16A ? 256.0f : 128.0f;
+  constexpr float UNIT = F16A ? 4.0f : 1.0f;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+  const int col = lane & 15, q = lane >> 4;
+
+  // ---- tile order: XCD-contiguous ranges, GROUP_M-swizzled inside --------
+  const int nbm = ceil_div(p.M, kBM), nbn = ceil_div(p.N, kBN);
+  const int total_tiles = nbm * nbn;
+  int bid = blockIdx.x;
+  if ((total_tiles & 7) == 0) bid = (bid & 7) * (total_tiles >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 8;
+  const int group = bid / (GROUP_M * nbn);
+  const int first = group * GROUP_M;
+  const int gm = min(nbm - first, GROUP_M);
+  const int in_group = bid - group * GROUP_M * nbn;
+  const int m0 = (first + in_group % gm) * kBM;
+  const int n0 = (in_group / gm) * kBN;
+
+  // ---- activation DMA plan: 32 segments (8 rows x 128 B) per stage --------
+  const int srow = lane >> 3;
+  const uint32_t smem_base = lds_addr_of(smem);
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  const int S = p.K / kKS;
+  auto dma_stage = [&](int s) {
+    const uint32_t slot = smem_base + (s & 1) * kStage;
+    static_for<0, 8>([&](auto i) {
+      const int seg = wave + 4 * i;
+      const int h = seg >> 4, rb = seg & 15;
+      const int row = rb * 8 + srow;
+      const uint32_t lc = static_cast<uint32_t>((lane & 7) ^ (row & 7));
+      int rg = min(m0 + row, p.M - 1);
+      asm volatile("" : "+v"(rg));
+      const uint32_t voff = static_cast<uint32_t>(rg) * static_cast<uint32_t>(2 * p.a_sm) + 128u * h + 16u * lc;
+      dma16s(a_base + static_cast<int64_t>(s) * 256, voff, slot + h * kHalf + rb * 1024);
+    });
+  };
+
+  // ---- weight loads of one stage ----------------------------------------
+  int ncol[kFN];
+  static_for<0, kFN>([&](auto t) { ncol[t] = min(n0 + wc * 64 + 16 * t + col, p.N - 1); });
+  const int KW = p.K >> 3;
+  auto load_w = [&](StageW<FMT>& sw, int s) {
+    static_for<0, kFN>([&](auto t) {
+      const uint32_t n = static_cast<uint32_t>(ncol[t]);
+      if constexpr (!W4) {
+        const uint32_t off = n * static_cast<uint32_t>(p.w8_sn) + 128u * s + 32u * q;
+        const i32x4 v0 = load_at<i32x4>(p.w8, off);
+        const i32x4 v1 = load_at<i32x4>(p.w8, off + 16);
+        static_for<0, 4>([&](auto e) {
+          sw.w[t][e] = static_cast<uint32_t>(v0[int(e)]);
+          sw.w[t][4 + e] = static_cast<uint32_t>(v1[int(e)]);
+        });
+      } else {
+        const int kw0 = 16 * s;
+        auto woff = [&](int kw) -> uint32_t {
+          return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (n * KW + kw);
+        };
+        if constexpr (!KN && G == 128) {
+          const i32x4 v = load_at<i32x4>(p.w4, woff(kw0 + 4 * q));
+          static_for<0, 4>([&](auto j) { sw.w[t][j] = static_cast<uint32_t>(v[int(j)]); });
+        } else if constexpr (!KN && G == 64) {
+          const uint2 v0 = load_at<uint2>(p.w4, woff(kw0 + 2 * q));
+          const uint2 v1 = load_at<uint2>(p.w4, woff(kw0 + 8 + 2 * q));
+          sw.w[t][0] = v0.x;
+          sw.w[t][1] = v0.y;
+          sw.w[t][2] = v1.x;
+          sw.w[t][3] = v1.y;
+        } else {
+          static_for<0, 4>([&](auto j) { sw.w[t][j] = load_at<uint32_t>(p.w4, woff(kw0 + word_of<G, KN>(q, j))); });
+        }
+        static_for<0, SPS>([&](auto g) {
+          const uint32_t gi = n * p.ng + s * SPS + g;
+          if constexpr (UINT4) {
+            sw.gs[t][g] = load_at<uint32_t>(p.scales, 4u * (gi >> 1));
+            sw.gz[t][g] = load_at<uint32_t>(p.zeros, 4u * (n * p.zw + ((s * SPS + g) >> 3)));
+          } else {
+            sw.gs[t][g] = load_at<uint32_t>(p.scales, p.scale_f32 ? 4u * gi : 4u * (gi >> 1));
+            sw.gz[t][g] = (p.flags & QG_W4_ZEROS_PACKED)
+                              ? load_at<uint32_t>(p.zeros, 4u * (n * p.zw + ((s * SPS + g) >> 3)))
+                              : load_at<uint32_t>(p.zeros, 4u * gi);
+          }
+        });
+      }
+    });
+  };
+
+  // ---- fragment read offsets (rows of this wave, per fragment f) -----------
+  // chunk f = word_of(q, j) of the stage: half f >> 3, logical 16-byte chunk f & 7
+  uint32_t a_row_off[kFM];
+  static_for<0, kFM>([&](auto f) {
+    const int r = wr * 64 + 16 * f + col;
+    a_row_off[f] = static_cast<uint32_t>(r * 128);
+  });
+  const int rsw = col & 7;  // (row & 7) of every row this lane reads
+
+  uint32_t sel[4], umask = F16A ? 0x00F000F0u : 0x000F000Fu, umagic = F16A ? 0x5C005C00u : 0x43004300u;
+  nat_selectors(W4 && !UINT4 && (p.flags & QG_W4_ORDER_HIGH), sel);
+  asm volatile("" : "+v"(umask), "+v"(umagic));
+  const uint32_t wxor = (W4 && !UINT4 && (p.flags & QG_W4_SIGNED_NIBBLES)) ? 0x88888888u : 0u;
+  const uint32_t ones2 = F16A ? 0x3C003C00u : 0x3F803F80u;
+  const i32x4 ones = {static_cast<int>(ones2), static_cast<int>(ones2), static_cast<int>(ones2),
+                      static_cast<int>(ones2)};
+
+  f32x4 acc[kFM][kFN];
+  f32x4 tot[W4 ? kFM : 1][W4 ? kFN : 1];
+  f32x4 asum[kFM];
+  static_for<0, kFM>([&](auto f) {
+    static_for<0, kFN>([&](auto t) { acc[f][t] = f32x4{0, 0, 0, 0}; });
+  });
+  if constexpr (W4) {
+    static_for<0, kFM>([&](auto f) {
+      static_for<0, kFN>([&](auto t) { tot[f][t] = f32x4{0, 0, 0, 0}; });
+    });
+  }
+
+  StageW<FMT> wcur, wnext;
+  if (S > 0) {
+    dma_stage(0);
+    load_w(wcur, 0);
+  }
+  for (int s = 0; s < S; ++s) {
+    wait_vm_barrier<0>();  // stage s landed everywhere; slot (s+1)&1 is free
+    if (s + 1 < S) {
+      dma_stage(s + 1);
+      load_w(wnext, s + 1);
+    }
+    const char* const sbuf = smem + (s & 1) * kStage;
+    static_for<0, 4>([&](auto j) {
+      if constexpr (W4 && j % STEPS_PER_GROUP == 0) {
+        static_for<0, kFM>([&](auto f) {
+          asum[f] = f32x4{0, 0, 0, 0};
+          static_for<0, kFN>([&](auto t) { acc[f][t] = f32x4{0, 0, 0, 0}; });
+        });
+      }
+      // activation fragments of step j
+      const int fw = W4 ? word_of<G, KN>(q, j) : 4 * q + j;
+      const uint32_t chunk_off = static_cast<uint32_t>((fw >> 3) * kHalf + (((fw & 7) ^ rsw) << 4));
+      i32x4 af[kFM];
+      static_for<0, kFM>([&](auto f) {
+        af[f] = *reinterpret_cast<const i32x4*>(sbuf + a_row_off[f] + chunk_off);
+      });
+      if constexpr (W4) static_for<0, kFM>([&](auto f) { asum[f] = mfma16<F16A>(af[f], ones, asum[f]); });
+      static_for<0, kFN>([&](auto t) {
+        i32x4 b;
+        if constexpr (W4) b = unpack_nat<F16A>(wcur.w[t][j] ^ wxor, sel, umask, umagic);
+        else b = fp8x8<F16A, FMT == WD_FP8_E5M2>(wcur.w[t][2 * j], wcur.w[t][2 * j + 1]);
+        static_for<0, kFM>([&](auto f) { acc[f][t] = mfma16<F16A>(af[f], b, acc[f][t]); });
+      });
+      if constexpr (W4 && j % STEPS_PER_GROUP == STEPS_PER_GROUP - 1) {
+        constexpr int gi = j / STEPS_PER_GROUP;
+        static_for<0, kFN>([&](auto t) {
+          const int g = s * SPS + gi;
+          const uint32_t i = static_cast<uint32_t>(ncol[t]) * p.ng + g;
+          float sc, zb;
+          const uint32_t rs = wcur.gs[t][gi], rz = wcur.gz[t][gi];
+          if constexpr (UINT4) {
+            sc = __uint_as_float((i & 1u) ? (rs & 0xFFFF0000u) : (rs << 16));
+            zb = MAGIC + UNIT * static_cast<float>((rz >> ((g & 7) * 4)) & 15u);
+          } else {
+            sc = p.scale_f32 ? __uint_as_float(rs) : __uint_as_float((i & 1u) ? (rs & 0xFFFF0000u) : (rs << 16));
+            const bool packed = p.flags & QG_W4_ZEROS_PACKED;
+            const int z = packed ? static_cast<int>((rz >> ((g & 7) * 4)) & 15u) : static_cast<int>(rz);
+            const int zu = (p.flags & QG_W4_SIGNED_NIBBLES) ? (packed ? (z ^ 8) : z + 8) : z;
+            zb = MAGIC + UNIT * static_cast<float>(zu);
+          }
+          sc = sc / UNIT;
+          static_for<0, kFM>([&](auto f) {
+            static_for<0, 4>([&](auto e) {
+              const float v = __builtin_fmaf(-zb, asum[f][int(e)], acc[f][t][int(e)]);
+              tot[f][t][int(e)] = __builtin_fmaf(sc, v, tot[f][t][int(e)]);
+            });
+          });
+        });
+      }
+    });
+    if (s + 1 < S) wcur = wnext;
+  }
+
+  // ---- epilogue -------------------------------------------------------------
+  static_for<0, kFN>([&](auto t) {
+    const int nn = n0 + wc * 64 + 16 * t + col;
+    if (nn < p.N) {
+      const float bv = p.bias ? bias_at(p.bias, p.bias_dtype, nn) : 0.0f;
+      const float ws = (!W4 && p.w_scale) ? p.w_scale[nn] : 1.0f;
+      static_for<0, kFM>([&](auto f) {
+        static_for<0, 4>([&](auto e) {
+          const int row = m0 + wr * 64 + 16 * f + 4 * q + e;
+          if (row < p.M) {
+            float v;
+            if constexpr (W4) v = tot[f][t][int(e)];
+            else {
+              v = acc[f][t][int(e)];
+              if (p.w_scale) v = v * ws;
+            }
+            if (p.bias) v = v + bv;
+            put_out(p.out, p.out_dtype, static_cast<int64_t>(row) * p.N + nn, v);
+          }
+        });
+      });
+    }
+  });
+}
+
+template <int FMT, int G, bool KN>
+hipError_t launch_wd_t(const WdArgs& p, hipStream_t stream) {
+  const int tiles = ceil_div(p.M, kBM) * ceil_div(p.N, kBN);
+  if (p.a_f16)
+    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, true>), dim3(tiles), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, false>), dim3(tiles), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+// dst[r, k] = src[r * s_r + k * s_k] (16-bit) for k < K, 0 for K <= k < k_pad.
+__global__ void k_pack_rows_u16(const uint16_t* src, int64_t s_r, int64_t s_k, int64_t rows, int64_t K,
+                                uint16_t* dst, int64_t k_pad) {
+  const int64_t total = rows * k_pad;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / k_pad, k = i % k_pad;
+    dst[i] = k < K ? src[r * s_r + k * s_k] : static_cast<uint16_t>(0);
+  }
+}
+
+// out[n, k] = decode(w[n * w_sn + k * w_sk]) in out_dtype: every finite OCP
+// fp8 value is exact in fp16, fp32 and bf16 (bit construction of fp8_to_f32).
+__global__ void k_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64_t n, int64_t K, int e5,
+                             void* out, int out_dtype) {
+  const int64_t total = n * K;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / K, k = i % K;
+    put_out(out, out_dtype, i, fp8_to_f32(w[r * w_sn + k * w_sk], e5 != 0));
+  }
+}
+
+unsigned grid_for(int64_t total) {
+  const int64_t blocks = ceil_div<int64_t>(total, 256);
+  return static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
+}
+
+}  // namespace
+
+hipError_t launch_pack_rows_u16(const uint16_t* src, int64_t s_r, int64_t s_k, int64_t rows, int64_t K,
+                                uint16_t* dst, int64_t k_pad, hipStream_t stream) {
+  if (rows * k_pad == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_pack_rows_u16, dim3(grid_for(rows * k_pad)), dim3(256), 0, stream, src, s_r, s_k, rows,
+                     K, dst, k_pad);
+  return hipGetLastError();
+}
+
+hipError_t launch_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64_t n, int64_t K, int e5,
+                             void* out, int out_dtype, hipStream_t stream) {
+  if (n * K == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fp8_decode, dim3(grid_for(n * K)), dim3(256), 0, stream, w, w_sn, w_sk, n, K, e5, out,
+                     out_dtype);
+  return hipGetLastError();
+}
+
+hipError_t launch_wd_fp8(const WdArgs& p, hipStream_t stream) {
+  return p.fp8_e5 ? launch_wd_t<WD_FP8_E5M2, 128, false>(p, stream)
+                  : launch_wd_t<WD_FP8_E4M3, 128, false>(p, stream);
+}
+
+hipError_t launch_wd_w4(const WdArgs& p, hipStream_t stream) {
+  const bool kn = p.flags & QG_W4_LAYOUT_KN;
+  const bool uint4 = !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED;
+  switch (p.group) {
+    case 128:
+      if (uint4 && !kn) return launch_wd_t<WD_W4_UINT4, 128, false>(p, stream);
+      return kn ? launch_wd_t<WD_W4_GENERIC, 128, true>(p, stream) : launch_wd_t<WD_W4_GENERIC, 128, false>(p, stream);
+    case 64:
+      return kn ? launch_wd_t<WD_W4_GENERIC, 64, true>(p, stream) : launch_wd_t<WD_W4_GENERIC, 64, false>(p, stream);
+    default:
+      return kn ? launch_wd_t<WD_W4_GENERIC, 32, true>(p, stream) : launch_wd_t<WD_W4_GENERIC, 32, false>(p, stream);
+  }
+}
+
+}  // namespace qg

@@ -186,3 +186,53 @@ def test_cfg2_decode_full_size(cuda, m):
     for out_dtype in (torch.bfloat16, torch.float32):
         y = w4().w4a16_gemm(a.to(cuda), p, out_dtype=out_dtype)
         check_product(y, y64, absmag, out_dtype, f"cfg2 m{m} {out_dtype}")
+
+
+@pytest.mark.parametrize("g", o4.GROUPS)
+@pytest.mark.parametrize("layout,order", [("nk", "low"), ("nk", "high"), ("kn", "low")])
+@pytest.mark.parametrize("adtype", [torch.float16, torch.bfloat16])
+def test_w4a16_tiled_all_formats(cuda, g, layout, order, adtype):
+    """M > 64 and K % 128 == 0: the tiled kernel (activation stages in LDS)."""
+    for m, n, sym, bias in ((200, 200, False, True), (129, 64, True, False)):
+        case(f"w4a16 tiled m{m} n{n} k384 g{g} {layout} {order} {adtype} sym={sym}")
+        _gemm_case(cuda, m, n, 384, g, sym, layout, order, adtype, bias, seed=m + g)
+
+
+def test_w4a16_tiled_uint4_and_f32_out(cuda):
+    case("w4a16 tiled uint4 storage, fp32 out")
+    rng = np.random.default_rng(12)
+    m, n, k = 300, 160, 1024
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    p = w4().pack_uint4(torch.from_numpy(w).to(cuda), group_size=128)
+    r = o4.pack_uint4_baseline(w, group_size=128)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    b = torch.from_numpy((rng.standard_normal(n) * 0.1).astype(np.float32)).to(torch.bfloat16)
+    av = act_values(a)
+    cen = o4.dequant_baseline(r, floating=False)
+    s = bf16_bits_to_f32(r["scales"])
+    y64 = o4.w4a16_linear(av, cen, s, 128, act_values(b))
+    absmag = o4.w4a16_linear(np.abs(av), np.ones_like(cen), s, 128)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        y = w4().w4a16_gemm(a.to(cuda), p, b.to(cuda), out_dtype=out_dtype)
+        check_product(y, y64, absmag, out_dtype, f"tiled uint4 {out_dtype}")
+
+
+def test_cfg2_prefill_full_size(cuda):
+    """BASELINE configuration 2, prefill M = 2048 at its real shape: every
+    output is finite and 256 rows spread over M are checked against the
+    float64 oracle."""
+    case("cfg2 w4a16 m2048 k4096 n14336")
+    g = torch.Generator().manual_seed(2)
+    w = (torch.randn(14336, 4096, generator=g) * 0.02)
+    a = torch.randn(2048, 4096, generator=g).to(torch.bfloat16)
+    p = w4().pack_uint4(w.to(cuda), group_size=128)
+    r = o4.pack_uint4_baseline(w.numpy(), group_size=128)
+    y = w4().w4a16_gemm(a.to(cuda), p)
+    assert torch.isfinite(y).all()
+    rows = np.linspace(0, 2047, 256).astype(int)
+    av = act_values(a)[rows]
+    cen = o4.dequant_baseline(r, floating=False)
+    s = bf16_bits_to_f32(r["scales"])
+    y64 = o4.w4a16_linear(av, cen, s, 128)
+    absmag = o4.w4a16_linear(np.abs(av), np.ones_like(cen), s, 128)
+    check_product(y[torch.from_numpy(rows).to(cuda)], y64, absmag, torch.bfloat16, "cfg2 prefill")

@@ -16,6 +16,10 @@ Prints one JSON line (driver contract). ``value`` = whole-chain TOPS
 (2*M*N*K summed over the three GEMMs, divided by the step time).
 ``roofline`` covers the dominant kernel (the int8 GEMM), timed with HIP events
 around each GEMM launch on its stream inside the timed steps.
+``roofline_w4a16_decode`` is the metric's second half: the W4A16 decode kernel
+(M = 1) in GB/s against the 8 TB/s HBM peak, timed
+with events around graph replays of 120 launches over 12 rotated weight copies.
+``secondary`` holds cfg0, W4A16 M = 16 / 2048 and the FP8 configuration 3.
 """
 from __future__ import annotations
 
@@ -34,6 +38,7 @@ for _p in (str(ROOT), str(PKG)):
 METRIC = "W8A8 INT8 GEMM TOPS (% MFMA peak); W4A16 decode HBM GB/s (% peak)"
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+PEAK_BF16_TFLOPS = 2500.0 # MI355X dense bf16 MFMA, 2.5 PFLOP/s
 
 
 def parse():
@@ -145,6 +150,82 @@ def run_cfg0(torch, lib, _lib, quantize, synthetic, dev, iters=50):
             "cfg0_w8a8_linear_tops": round(lin_tops, 1)}
 
 
+def _graph_time(torch, fn, launches, replays=4):
+    """Capture ``launches`` calls of fn(i) in a HIP graph on a side stream and
+    return the average time per call (ms) over ``replays`` replays, timed with
+    events on that stream (no host launch cost inside the timed region)."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for i in range(4):
+            fn(i, s.cuda_stream)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(launches):
+                fn(i, s.cuda_stream)
+        g.replay()
+        s.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(replays):
+            g.replay()
+        e1.record(s)
+        e1.synchronize()
+    return e0.elapsed_time(e1) / (launches * replays)
+
+
+def run_w4a16(torch, lib, _lib, dev, copies=12):
+    """W4A16, K 4096, N 14336, group 128, uint4
+    storage with bf16 scales and uint4 zero points, bf16 activations / out.
+    Decode (M = 1, 16) rotates over ``copies`` weight copies (> 256 MB, more than
+    the MALL) so every launch streams its weights from HBM."""
+    from rdna2_ops import int4_weight_gemm_v07 as w4
+    N, K, G = 14336, 4096, 128
+    gen = torch.Generator().manual_seed(2)
+    p0 = w4.pack_uint4((torch.randn(N, K, generator=gen) * 0.02).to(dev), group_size=G)
+    ps = [p0] + [w4.PackedInt4(p0.data.clone(), p0.scales.clone(), p0.zeros.clone(), p0.sums, N, K, G, False,
+                               signed=False, zeros_packed=True) for _ in range(copies - 1)]
+    wbytes = p0.data.numel() * 4 + p0.scales.numel() * 2 + p0.zeros.numel() * 4
+    P = _lib.ptr
+    out = {}
+    for m in (1, 16, 2048):
+        a = torch.randn(m, K, generator=gen).to(torch.bfloat16).to(dev)
+        y = torch.empty(m, N, dtype=torch.bfloat16, device=dev)
+
+        def call(i, stream, a=a, y=y, m=m):
+            p = ps[i % copies] if m <= 16 else p0
+            _lib.check(lib.qg_w4a16_gemm(P(a), _lib.BF16, K, m, K, P(p.data), N, G, p.flags, P(p.scales), _lib.BF16,
+                                         P(p.zeros), None, 0, P(y), _lib.BF16, None, 0, stream), "w4a16")
+        ms = _graph_time(torch, call, 120 if m <= 16 else 10, replays=4 if m <= 16 else 2)
+        bytes_ = wbytes + m * K * 2 + m * N * 2
+        out[m] = {"us": round(ms * 1e3, 2), "GBs": round(bytes_ / (ms * 1e-3) / 1e9, 1),
+                  "frac_hbm_peak": round(bytes_ / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                  "TFLOPs": round(2 * m * N * K / (ms * 1e-3) / 1e12, 1), "bytes": bytes_}
+    return out
+
+
+def run_fp8(torch, lib, _lib, dev):
+    """e4m3 weights with per-channel absmax/448 scales,
+    bf16 activations M 4096, K 3072, N 3072 and 12288, bf16 out."""
+    from rdna2_ops import fp8_weight_gemm_v06 as f8
+    gen = torch.Generator().manual_seed(3)
+    res = {}
+    for n in (3072, 12288):
+        m, k = 4096, 3072
+        codes, sc = f8.quantize_weight_e4m3((torch.randn(n, k, generator=gen) * 0.02).to(dev))
+        a = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        P = _lib.ptr
+
+        def call(i, stream, a=a, y=y, codes=codes, sc=sc, n=n):
+            _lib.check(lib.qg_fp8w_gemm(P(a), _lib.BF16, k, 1, m, k, P(codes), _lib.E4M3, k, 1, n, P(sc), None, 0,
+                                        P(y), _lib.BF16, None, 0, stream), "fp8w")
+        ms = _graph_time(torch, call, 10, replays=2)
+        tf = 2 * m * n * k / (ms * 1e-3) / 1e12
+        res[n] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    return res
+
+
 def traffic_bytes():
     """HBM bytes per launch of the GEMM kernel in this chain, measured with
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a plain-copy calibration)
@@ -225,12 +306,30 @@ def main():
                      "per_launch": layer_info},
     }
     if not args.no_secondary:
-        line["secondary"] = run_cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev)
+        sec = run_cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev)
+        w4 = run_w4a16(torch, lib, _lib, dev)
+        dec = w4[1]
+        # second half of the headline metric: W4A16 decode (M = 1) HBM GB/s
+        line["roofline_w4a16_decode"] = {
+            "bound": "hbm", "achieved": dec["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": dec["frac_hbm_peak"], "traffic": None,
+            "kernel": "k_w4_decode<1,2,128> (M=1, K 4096, N 14336, g128 uint4, 12 rotated weight copies)",
+            "us_per_launch": dec["us"], "algorithmic_bytes": dec["bytes"]}
+        sec["w4a16_m1"] = w4[1]
+        sec["w4a16_m16"] = w4[16]
+        sec["w4a16_prefill_m2048"] = w4[2048]
+        sec["fp8_cfg3"] = run_fp8(torch, lib, _lib, dev)
+        line["secondary"] = sec
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import time_cfg1_chain
         cpu_ops, cpu_s, threads, sample = time_cfg1_chain(rows=args.cpu_rows, seconds=args.cpu_seconds)
         line["cpu_baseline"] = {"value": round(cpu_ops / 1e12, 4), "unit": "TOPS", "cores": threads,
                                 "kind": "port", "sample": sample, "seconds_per_sample": round(cpu_s, 3)}
+        if not args.no_secondary:
+            from oracle.cpu_baseline import time_w4a16_decode
+            gbs, sec_s, threads, sample = time_w4a16_decode(seconds=min(5.0, args.cpu_seconds))
+            line["cpu_baseline_w4a16_decode"] = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads,
+                                                 "kind": "port", "sample": sample}
     print(json.dumps(line), flush=True)
 
 

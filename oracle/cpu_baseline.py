@@ -71,3 +71,35 @@ def time_cfg1_chain(rows=4096, hidden=3072, threads=None, seconds=10.0, seed=1):
     ops = 2 * rows * hidden * (3 * hidden + 4 * hidden + 4 * hidden)
     return ops / sec, sec, threads, (f"cfg1 chain on {rows} of 4096 tokens, torch CPU int8 (_int_mm), "
                                      f"median of {len(times)} passes in {time.perf_counter() - start:.1f} s")
+
+
+def time_w4a16_decode(n=14336, k=4096, group=128, seconds=5.0, seed=2, threads=None):
+    """CPU formulation of the W4A16 decode (M = 1):
+    dequantise the uint4 weight (q - z) * s to fp32, F.linear in fp32, cast to
+    bf16 — as restated in BASELINE's CPU-baseline plan. Repeated for about
+    ``seconds``; returns (GB/s of the packed weight streamed, median seconds,
+    threads, sample description)."""
+    threads = threads or len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randint(0, 16, (n, k), generator=g, dtype=torch.uint8)
+    z = torch.randint(0, 16, (n, k // group), generator=g, dtype=torch.uint8)
+    s = (torch.rand(n, k // group, generator=g) * 1e-3).to(torch.bfloat16)
+    a = torch.randn(1, k, generator=g).to(torch.bfloat16)
+
+    def once():
+        w = (q.view(n, k // group, group).float() - z.float()[..., None]) * s.float()[..., None]
+        return torch.nn.functional.linear(a.float(), w.view(n, k)).to(torch.bfloat16)
+
+    once()
+    times = []
+    start = time.perf_counter()
+    while len(times) < 2 or time.perf_counter() - start < seconds:
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    sec = times[len(times) // 2]
+    wbytes = n * k // 2 + n * (k // group) * 2 + n * ((k // group + 7) // 8) * 4
+    return wbytes / sec / 1e9, sec, threads, (f"W4A16 M=1 K={k} N={n} g{group}, torch CPU dequant + fp32 "
+                                               f"F.linear, median of {len(times)} passes")

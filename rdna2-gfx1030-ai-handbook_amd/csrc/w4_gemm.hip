@@ -18,8 +18,6 @@
 #include "qg_common.h"
 #include "qg_internal.h"
 
-#include <stdlib.h>
-
 namespace qg {
 
 namespace {
@@ -585,128 +583,6 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
   }
 }
 
-// --------------------------------------------------------------- GEMV kernel
-// M == 1, group 128, "nk" words, K <= 4096: the token-decode shape of
-// BASELINE configuration 2. One wave per workgroup and per 16-column tile,
-// over the whole K, so there is no cross-wave reduction and no barrier:
-//   1. the wave issues every load it needs at once — its activation rows
-//      (LDS staging), its columns' scales and zero points (a few 16-byte
-//      loads, 32 groups each) and all <= 32 chunks of weight words;
-//   2. it stores the activation rows to its private LDS region in even/odd
-//      order (see the decode kernel) while the weights stream in;
-//   3. it consumes the chunks in issue order, each as soon as it has landed;
-//      the per-row group sums come from an MFMA against ones;
-//   4. lanes 0-15 write their column's rows.
-// Storage formats: UINT4 (bf16 scales, packed unsigned zero points) or the
-// reference's fp32 scales + int32 zero points (signed or unsigned nibbles,
-// low or high order).
-constexpr int kGemvChunks = 32;
-
-template <int RP, bool F16A, bool UINT4>
-__global__ __launch_bounds__(64) void k_w4_gemv(W4Args p) {
-#pragma clang fp contract(off)
-  constexpr int D = kGemvChunks;
-  constexpr int ROWB = D * 128 * 2 + 16;        // LDS bytes per staged row (padded)
-  constexpr float MAGIC = F16A ? 256.0f : 128.0f;
-  constexpr float UNIT = F16A ? 4.0f : 1.0f;
-  constexpr int NI = RP == 1 ? 1 : 4;           // accumulator registers with real rows
-  constexpr int SV = UINT4 ? D / 8 : D / 4;     // 16-byte scale vectors (8 bf16 / 4 fp32)
-  constexpr int ZV = UINT4 ? 1 : D / 4;         // 16-byte zero-point vectors
-  const uint32_t ones2 = F16A ? 0x3C003C00u : 0x3F803F80u;
-  __shared__ __attribute__((aligned(16))) char a_lds[RP * ROWB];
-
-  const int lane = threadIdx.x;
-  const int col = lane & 15, q = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  const int n = min(n0 + col, p.N - 1);
-  const int m0 = blockIdx.y * RP;
-  const int R = min(p.M - m0, RP);
-  const int C = ceil_div(p.K, 128);
-  const int KW = p.K >> 3;
-
-  // ---- 1. every load of the wave ------------------------------------------
-  i32x4 av[RP][D / 4];  // activation rows: lane covers K [8 lane + 512 v, +8)
-  static_for<0, RP>([&](auto r) {
-    const uint32_t roff = 2u * static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.a_sm);
-    static_for<0, D / 4>([&](auto v) {
-      const int k = min(512 * v + 8 * lane, p.K - 8);
-      av[r][v] = load_at<i32x4>(p.a, roff + 2u * k);
-    });
-  });
-  i32x4 sv[SV], zv[ZV];
-  static_for<0, SV>([&](auto v) {
-    const int per = UINT4 ? 8 : 4;  // groups per vector
-    const int g = min(per * v, p.ng - per);
-    sv[v] = load_at<i32x4>(p.scales, (UINT4 ? 2u : 4u) * (static_cast<uint32_t>(n) * p.ng + g));
-  });
-  static_for<0, ZV>([&](auto v) {
-    if constexpr (UINT4) {
-      zv[v] = load_at<i32x4>(p.zeros, 4u * (static_cast<uint32_t>(n) * p.zw));
-    } else {
-      const int g = min(4 * v, p.ng - 4);
-      zv[v] = load_at<i32x4>(p.zeros, 4u * (static_cast<uint32_t>(n) * p.ng + g));
-    }
-  });
-  i32x4 w[D];
-  static_for<0, D>([&](auto c) {
-    w[c] = load_at<i32x4>(p.w, 4u * (static_cast<uint32_t>(n) * KW + min(16 * c, KW - 16) + 4 * q));
-  });
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- 2. activations -> LDS, even/odd order -------------------------------
-  static_for<0, RP>([&](auto r) {
-    static_for<0, D / 4>([&](auto v) {
-      *reinterpret_cast<i32x4*>(a_lds + r * ROWB + 1024 * v + 16 * lane) = even_odd(av[r][v]);
-    });
-  });
-
-  Unpack7<F16A, UINT4> unpack;
-  unpack.init(!UINT4 && (p.flags & QG_W4_ORDER_HIGH));
-  const uint32_t wxor = (!UINT4 && (p.flags & QG_W4_SIGNED_NIBBLES)) ? 0x88888888u : 0u;
-  const i32x4 ones = {static_cast<int>(ones2), static_cast<int>(ones2), static_cast<int>(ones2),
-                      static_cast<int>(ones2)};
-  const char* const arow = a_lds + min(col, R - 1) * ROWB;
-  f32x4 total = {0, 0, 0, 0};
-
-  // ---- 3. chunk c = group c --------------------------------------------------
-  static_for<0, D>([&](auto c) {
-    f32x4 acc = {0, 0, 0, 0}, asum = {0, 0, 0, 0};
-    static_for<0, 4>([&](auto j) {
-      const i32x4 af = *reinterpret_cast<const i32x4*>(arow + 2 * (c * 128 + 8 * (4 * q + j)));
-      asum = mfma16<F16A>(af, ones, asum);
-      acc = mfma16<F16A>(af, unpack(UINT4 ? static_cast<uint32_t>(w[c][int(j)])
-                                          : static_cast<uint32_t>(w[c][int(j)]) ^ wxor), acc);
-    });
-    float s, zb;
-    if constexpr (UINT4) {
-      const uint32_t sw = static_cast<uint32_t>(sv[c / 8][(c % 8) / 2]);
-      s = __uint_as_float((c & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
-      zb = MAGIC + UNIT * static_cast<float>((static_cast<uint32_t>(zv[0][c / 8]) >> (4 * (c % 8))) & 15u);
-    } else {
-      s = __int_as_float(sv[c / 4][c % 4]);
-      int z = zv[c / 4][c % 4];
-      if (p.flags & QG_W4_SIGNED_NIBBLES) z += 8;
-      zb = MAGIC + UNIT * static_cast<float>(z);
-    }
-    s = (c < C) ? s / UNIT : 0.0f;  // chunks past K were re-read, not counted
-    static_for<0, NI>([&](auto i) {
-      const float v = __builtin_fmaf(-zb, asum[int(i)], acc[int(i)]);
-      total[int(i)] = __builtin_fmaf(s, v, total[int(i)]);
-    });
-  });
-
-  // ---- 4. lanes 0-15: rows 0..3 of column n0 + col -------------------------
-  if (q == 0 && n0 + col < p.N) {
-    static_for<0, NI>([&](auto i) {
-      if (i < R) {
-        float v = total[int(i)];
-        if (p.bias) v = v + load_bias(p.bias, p.bias_dtype, n0 + col);
-        store_out(p.out, p.out_dtype, static_cast<int64_t>(m0 + i) * p.N + n0 + col, v);
-      }
-    });
-  }
-}
-
 // ------------------------------------------------------------ pack / unpack
 // One thread per (column n, octet of 8 groups): the zero points of an octet
 // share one packed word. Rule of _pack_weight (int4_weight_gemm_v07.py:103-133)
@@ -860,37 +736,13 @@ hipError_t launch_decode_g(const W4Args& p, hipStream_t stream) {
   }
 }
 
-// The GEMV kernel serves M == 1, group 128, "nk", K <= 4096 with scale /
-// zero-point rows that start on 16-byte boundaries (more activation rows do
-// not fit in registers next to the 32 chunks of weight words).
-bool gemv_fits(const W4Args& p) {
-  if (p.M != 1 || p.group != 128 || (p.flags & QG_W4_LAYOUT_KN) || p.K > kGemvChunks * 128) return false;
-  const bool uint4 = !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED;
-  const bool ref = p.scale_f32 && !(p.flags & QG_W4_ZEROS_PACKED);
-  if (uint4) return p.ng % 8 == 0 && p.zw % 4 == 0 && p.ng >= 8;
-  return ref && p.ng % 4 == 0 && p.ng >= 4;
-}
-
-template <bool F16A>
-hipError_t launch_gemv(const W4Args& p, hipStream_t stream) {
-  const bool uint4 = !p.scale_f32;
-  dim3 grid(ceil_div(p.N, 16), p.M);
-  if (uint4) hipLaunchKernelGGL((k_w4_gemv<1, F16A, true>), grid, dim3(64), 0, stream, p);
-  else hipLaunchKernelGGL((k_w4_gemv<1, F16A, false>), grid, dim3(64), 0, stream, p);
-  return hipGetLastError();
-}
-
 template <bool F16A>
 hipError_t launch_skinny(const W4Args& p, hipStream_t stream) {
   const int C = ceil_div(p.K, 128);
-  const char* env_path = getenv("QG_W4_PATH");  // tuning knob while the variants are measured
-  const int path = env_path ? atoi(env_path) : 0;  // 0 auto, 2 decode, 3 skinny
-  if (path == 0 && gemv_fits(p)) return launch_gemv<F16A>(p, stream);
-  if (path == 3) return launch_skinny_g<1, 4, F16A>(p, stream);
   if (p.M <= 16 && ceil_div(C, 8) <= kDecodeChunks) {
-    const char* env_ct = getenv("QG_W4_CT");
-    const int ct = env_ct ? atoi(env_ct) : 0;
-    if (p.M == 1) return ct == 4 ? launch_decode_g<1, 4, F16A>(p, stream) : launch_decode_g<1, 2, F16A>(p, stream);
+    // one activation row: two column tiles per wave keep twice the waves in
+    // flight; 4 or 16 rows: four tiles share each activation fragment
+    if (p.M == 1) return launch_decode_g<1, 2, F16A>(p, stream);
     if (p.M <= 4) return launch_decode_g<4, 4, F16A>(p, stream);
     return launch_decode_g<16, 4, F16A>(p, stream);
   }

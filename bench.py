@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--only", choices=("w4a16", "fp8"), default=None,
+                    help="run one secondary measurement alone and print it (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -226,11 +228,11 @@ def run_fp8(torch, lib, _lib, dev):
     return res
 
 
-def traffic_bytes():
-    """HBM bytes per launch of the GEMM kernel in this chain, measured with
-    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a plain-copy calibration)
-    and recorded in profiles/int8_gemm_cfg1_chain_traffic.json; None if absent."""
-    path = ROOT / "profiles" / "int8_gemm_cfg1_chain_traffic.json"
+def traffic_bytes(name="int8_gemm_cfg1_chain_traffic.json"):
+    """HBM bytes per launch of a kernel, measured with rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE (scaled by a plain-copy calibration) and recorded in
+    profiles/<name>; None if absent."""
+    path = ROOT / "profiles" / name
     try:
         return json.loads(path.read_text())["hbm_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
@@ -260,6 +262,10 @@ def main():
         print(json.dumps({"copy_calibration_bytes_each_way": src.numel() * 4, "launches": 5}), flush=True)
         return
     lib = _lib.library()
+    if args.only:
+        res = run_w4a16(torch, lib, _lib, dev) if args.only == "w4a16" else run_fp8(torch, lib, _lib, dev)
+        print(json.dumps({"only": args.only, "result": res}), flush=True)
+        return
     chain = Chain(torch, lib, _lib, quantize_int8_rowwise, synthetic.cfg1(), dev)
     for _ in range(args.warmup):
         chain.step()
@@ -312,7 +318,7 @@ def main():
         # second half of the headline metric: W4A16 decode (M = 1) HBM GB/s
         line["roofline_w4a16_decode"] = {
             "bound": "hbm", "achieved": dec["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": dec["frac_hbm_peak"], "traffic": None,
+            "frac": dec["frac_hbm_peak"], "traffic": traffic_bytes("w4a16_decode_cfg2_traffic.json"),
             "kernel": "k_w4_decode<1,2,128> (M=1, K 4096, N 14336, g128 uint4, 12 rotated weight copies)",
             "us_per_launch": dec["us"], "algorithmic_bytes": dec["bytes"]}
         sec["w4a16_m1"] = w4[1]

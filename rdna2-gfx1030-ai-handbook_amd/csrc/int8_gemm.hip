@@ -3,28 +3,40 @@
 // epilogue order of rdna2-ops/rdna2_ops/comfy_int8.py:128-143).
 //
 // Design (MI355X-first, not a translation of the reference's Triton tiles):
-//  * one 256-thread workgroup (4 waves, 2x2) per BM x BN output tile; each wave
-//    owns a (BM/2) x (BN/2) sub-tile held in 16x16 int32 MFMA accumulators;
+//  * one workgroup per BM x BN output tile, its waves on a WGM x WGN grid;
+//    each wave owns a (BM/WGM) x (BN/WGN) sub-tile held in 32x32 int32 MFMA
+//    accumulators (v_mfma_i32_32x32x32_i8, 16 accumulator registers each);
 //  * operands are A [M, K] and W [N, K], both K-contiguous ("NT"), so every
-//    lane feeds v_mfma_i32_16x16x64_i8 with 16 contiguous K bytes;
-//  * K advances in 128-byte stages (two 64-byte MFMA sub-steps). Each stage
-//    of A and W is copied straight from HBM into a 2-slot LDS ring with
+//    lane feeds the MFMA with 16 contiguous K bytes of one row;
+//  * K advances in 128-byte stages (four 32-byte MFMA k-steps). Each stage of
+//    A and W is copied straight from HBM into a 2-slot LDS ring with
 //    global_load_lds_dwordx4, 8 rows x 128 B (whole cache lines) per wave
 //    instruction — the access pattern that sustains the most L2->LDS bandwidth
 //    per CU on gfx950;
-//  * software pipeline: a stage is read from LDS into registers while the
-//    MFMAs of the previous stage run; as soon as every wave holds it, its slot
-//    is refilled two stages ahead, so two stages (2 x 56 KB) stay in flight
-//    behind the MFMAs;
+//  * the direct copy path sustains ~37 B/clk per CU (one 1 KB copy per ~28
+//    cycles) whatever the depth in flight, about what a 256 x 192 tile needs at
+//    the full MFMA rate, and a wave blocked issuing a copy cannot issue MFMAs.
+//    Two pipelines:
+//      - 8 waves (2 per SIMD, 64 x 96 each) read each 32-byte k-step's
+//        fragments from LDS just in time; one barrier per stage; while one
+//        wave of a SIMD waits on a copy the other keeps the MFMA pipe busy
+//        (large problems);
+//      - 4 waves (1 per SIMD) stage the whole next stage in registers while
+//        the current one computes, two barriers per stage (small tiles, two
+//        workgroups per CU);
+//    Waits are branch-free: past the end the last stage is re-copied into its
+//    own slot (identical bytes, never a different stage's);
 //  * LDS rows are 128 bytes with the 16-byte chunk index XOR-swizzled by
-//    (row & 7): the DMA writes and the fragment reads (8 consecutive lanes =
-//    8 distinct 16-byte bank groups) are bank-conflict free;
+//    ((row >> 1) & 7): the DMA writes whole 1 KB blocks and every group of 16
+//    lanes of a fragment read touches 16 distinct 16-byte bank groups;
 //  * the linear block id is remapped so that each of the 8 XCDs (round-robin
 //    workgroup dispatch) walks one contiguous, GROUP_M-ordered range of tiles,
 //    keeping the A rows and W columns it shares in its own L2;
-//  * the epilogue is specialised at compile time (output dtype x order) and,
-//    for full tiles, stages the rounded tile through LDS so that HBM sees
-//    coalesced 16-byte row stores.
+//  * the per-row / per-column scales and the bias are fetched into registers
+//    before the K loop and parked in LDS for the epilogue, which is
+//    specialised at compile time (output dtype x order) and, for full tiles,
+//    stages the rounded tile through LDS so that HBM sees coalesced 16-byte
+//    row stores.
 #include "qg_common.h"
 #include "qg_internal.h"
 
@@ -32,22 +44,33 @@ namespace qg {
 
 namespace {
 
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
 enum EpiMode { EPI_INT = 0, EPI_F = 1, EPI_FMA = 2, EPI_EAGER = 3, EPI_GELU = 4 };
 
-template <int BM, int BN>
-struct I8Tile {
-  static constexpr int WM = BM / 2, WN = BN / 2;  // wave sub-tile
-  static constexpr int FM = WM / 16, FN = WN / 16;  // 16x16 fragments per wave
-  static constexpr int KS = 128;                   // K bytes per stage (2 MFMA sub-steps)
+// Tile geometry: BM x BN output tile, WGM x WGN waves, A ring of NA slots and
+// W ring of 2 slots of 128-byte K stages, epilogue parameters after the rings.
+template <int BM_, int BN_, int WGM, int WGN, int NA_>
+struct I8Geo {
+  static constexpr int BM = BM_, BN = BN_, NA = NA_;
+  static constexpr int NW = WGM * WGN, THREADS = 64 * NW;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave sub-tile
+  static constexpr int FM = WM / 32, FN = WN / 32;    // 32x32 blocks per wave
+  static constexpr int KS = 128;                      // K bytes per stage
+  static constexpr int KT = KS / 32;                  // MFMA k-steps per stage
   static constexpr int STAGE_A = BM * KS, STAGE_B = BN * KS;
-  static constexpr int STAGE = STAGE_A + STAGE_B;
-  static constexpr int NST = 2;                    // LDS ring depth
-  static constexpr int SEGS = (BM + BN) / 8;       // 1 KB DMA segments (8 rows x 128 B)
-  static constexpr int SPW = SEGS / 4;             // segments per wave
-  static constexpr int LDS_BYTES = NST * STAGE;
-  static_assert(BM % 32 == 0 && BN % 32 == 0, "tile must split into 2x2 waves of 16-multiples");
-  static_assert(SEGS % 4 == 0, "DMA segments must divide over 4 waves");
-  static_assert(SPW <= 2 * FM, "DMA issue is spread over the second-half fragment rows");
+  static constexpr int A_SEGS = BM / 8 / NW, B_SEGS = BN / 8 / NW;  // 1 KB copies per wave and stage
+  static constexpr int SPW = A_SEGS + B_SEGS;
+  static constexpr int RING_B = NA * STAGE_A;
+  static constexpr int RING = RING_B + 2 * STAGE_B;
+  static constexpr int SC_A = RING;
+  static constexpr int SC_B = SC_A + BM * 4;
+  static constexpr int SC_BIAS = SC_B + BN * 4;
+  static constexpr int LDS_BYTES = SC_BIAS + BN * 4;
+  static_assert(NA == 2 || NA == 3, "A ring depth");
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave sub-tile of 32x32 blocks");
+  static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0 && NW % 2 == 0, "copies split evenly over waves");
+  static_assert(BM <= THREADS && BN <= THREADS, "one epilogue parameter per thread");
 };
 
 __device__ __forceinline__ float gelu_tanh(float x) {
@@ -65,10 +88,14 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + t);
 }
 
-__device__ __forceinline__ float load_bias(const void* bias, int dtype, int col) {
-  if (dtype == QG_F32) return static_cast<const float*>(bias)[col];
-  const uint16_t b = static_cast<const uint16_t*>(bias)[col];
-  return dtype == QG_F16 ? f16_to_f32(b) : bf16_to_f32(b);
+// Raw storage bits of bias[col] (fp32, fp16 or bf16) and their fp32 value.
+__device__ __forceinline__ uint32_t load_bias_bits(const void* bias, int dtype, int col) {
+  if (dtype == QG_F32) return static_cast<const uint32_t*>(bias)[col];
+  return static_cast<const uint16_t*>(bias)[col];
+}
+__device__ __forceinline__ float bias_value(uint32_t bits, int dtype) {
+  if (dtype == QG_F32) return __uint_as_float(bits);
+  return dtype == QG_F16 ? f16_to_f32(static_cast<uint16_t>(bits)) : bf16_to_f32(static_cast<uint16_t>(bits));
 }
 
 template <int OUT>
@@ -117,17 +144,11 @@ __device__ __forceinline__ void store_elem(void* out, int64_t idx, uint32_t bits
   else static_cast<uint16_t*>(out)[idx] = static_cast<uint16_t>(bits);
 }
 
-template <int BM, int BN, int WPE, int OUT, int MODE>
-__global__ __launch_bounds__(256, WPE) void k_i8_gemm(I8GemmArgs p) {
-#pragma clang fp contract(off)
-  using T = I8Tile<BM, BN>;
-  __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-  const int wr = wave >> 1, wc = wave & 1;
-
-  // ---- tile order: XCD-contiguous ranges, GROUP_M-swizzled inside ---------
+// Output tile of this workgroup: the linear block id is remapped so that each
+// of the 8 XCDs (round-robin workgroup dispatch) walks one contiguous range of
+// tiles, GROUP_M-ordered inside.
+template <int BM, int BN>
+__device__ __forceinline__ void tile_origin(const I8GemmArgs& p, int& m0, int& n0) {
   const int nbm = ceil_div(p.M, BM), nbn = ceil_div(p.N, BN);
   const int total = nbm * nbn;
   int bid = blockIdx.x;
@@ -137,122 +158,293 @@ __global__ __launch_bounds__(256, WPE) void k_i8_gemm(I8GemmArgs p) {
   const int first = group * GROUP_M;
   const int gm = min(nbm - first, GROUP_M);
   const int in_group = bid - group * GROUP_M * nbn;
-  const int m0 = (first + in_group % gm) * BM;
-  const int n0 = (in_group / gm) * BN;
+  m0 = (first + in_group % gm) * BM;
+  n0 = (in_group / gm) * BN;
+}
 
-  // ---- DMA plan: this wave copies SPW 1 KB segments per stage --------------
-  // Segment seg = wave + 4 i covers 8 rows: A rows for seg < BM/8, W rows
-  // after. Lane l lands on LDS row (l >> 3) of the segment, physical chunk
-  // (l & 7), and fetches the logical chunk that the swizzle stores there.
-  // Offsets are 32-bit bytes from the operand base (operands < 2 GiB); they are
-  // recomputed per copy from two base rows to keep registers for fragments.
-  constexpr int A_SEGS_PER_WAVE = BM / 32;  // i < this: A segment
-  static_assert((BM / 8) % 4 == 0 && (BN / 8) % 4 == 0, "segments split evenly over waves");
-  const int srow = lane >> 3;
-  const uint32_t schunk16 = static_cast<uint32_t>(((lane & 7) ^ srow) << 4);
-  const int row_a = m0 + wave * 8 + srow;
-  const int row_w = n0 + wave * 8 + srow;
-  const uint32_t smem_base = lds_addr_of(smem);
-  const int S = p.K / T::KS;
-  const char* a_base = reinterpret_cast<const char*>(p.a);
-  const char* w_base = reinterpret_cast<const char*>(p.w);
-  auto dma = [&](auto i_c, int s) {
-    constexpr int i = decltype(i_c)::value;
-    const int64_t k = static_cast<int64_t>(s) * T::KS;
-    const uint32_t slot = smem_base + (s & 1) * T::STAGE;
-    // The opaque copy keeps the compiler from hoisting the 14 loop-invariant
+// Copies of one operand: segment i of a wave covers 8 rows starting at row
+// 8 (wave + NW i) of the tile. Lane l lands on LDS row 8 (wave + NW i) + (l >> 3),
+// physical 16-byte chunk (l & 7), and fetches the logical chunk that the
+// swizzle stores there: ((row >> 1) & 7) = 4 (wave & 1) + (l >> 4) for even NW.
+// Offsets are 32-bit bytes from the operand base (operands < 2 GiB), recomputed
+// per copy from one base row to keep registers for fragments.
+template <int NW>
+struct CopyPlan {
+  uint32_t chunk16;
+  int row0;
+  __device__ __forceinline__ CopyPlan(int tile_row0, int wave, int lane)
+      : chunk16(static_cast<uint32_t>(((lane & 7) ^ (4 * (wave & 1) + (lane >> 4))) << 4)),
+        row0(tile_row0 + wave * 8 + (lane >> 3)) {}
+  // Copy segment i of K stage s (K bytes [128 s, 128 s + 128)) of rows < rows
+  // (clamped) with row stride `stride` into LDS at slot_addr.
+  template <int I>
+  __device__ __forceinline__ void copy(const char* base, int64_t stride, int rows, int s, uint32_t slot_addr,
+                                       int wave) const {
+    int r = row0;
+    // The opaque copy keeps the compiler from hoisting the loop-invariant
     // offsets out of the K loop (they would be held in registers, or spilled).
-    int ra = row_a, rw = row_w;
-    asm volatile("" : "+v"(ra), "+v"(rw));
-    if constexpr (i < A_SEGS_PER_WAVE) {
-      const uint32_t row = static_cast<uint32_t>(min(ra + 32 * i, p.M - 1));
-      dma16s(a_base + k, row * static_cast<uint32_t>(p.a_sm) + schunk16,
-             slot + (wave + 4 * i) * 1024);
-    } else {
-      constexpr int iw = i - A_SEGS_PER_WAVE;
-      const uint32_t row = static_cast<uint32_t>(min(rw + 32 * iw, p.N - 1));
-      dma16s(w_base + k, row * static_cast<uint32_t>(p.w_sn) + schunk16,
-             slot + T::STAGE_A + (wave + 4 * iw) * 1024);
+    asm volatile("" : "+v"(r));
+    const uint32_t row = static_cast<uint32_t>(min(r + 8 * NW * I, rows - 1));
+    dma16s(base + static_cast<int64_t>(s) * 128, row * static_cast<uint32_t>(stride) + chunk16,
+           slot_addr + (wave + NW * I) * 1024);
+  }
+};
+
+// Fragment offset in an operand slot: k-step t, lane l reads row (l & 31) of a
+// 32-row block, logical chunk 2t + (l >> 5), stored at chunk ^ ((l >> 1) & 7).
+__device__ __forceinline__ int frag_offset(int t, int lane) {
+  return (lane & 31) * 128 + (((2 * t + (lane >> 5)) ^ ((lane >> 1) & 7)) << 4);
+}
+
+// Per-row / per-column epilogue parameters: thread t fetches row m0 + t's scale
+// and column n0 + t's scale and bias bits (indices clamped in range; values of
+// rows / columns past the edge are never stored).
+struct EpiParams {
+  float sa = 0.0f, sb = 0.0f;
+  uint32_t bias = 0;
+};
+template <int BM, int BN, int MODE>
+__device__ __forceinline__ EpiParams fetch_epi_params(const I8GemmArgs& p, int m0, int n0, int tid) {
+  EpiParams e;
+  if constexpr (MODE != EPI_INT) {
+    if (tid < BM) e.sa = p.a_scale[min(m0 + tid, p.M - 1)];
+    if (tid < BN) {
+      const int col = min(n0 + tid, p.N - 1);
+      e.sb = p.b_scale[p.b_scalar ? 0 : col];
+      if (p.bias != nullptr) e.bias = load_bias_bits(p.bias, p.bias_dtype, col);
     }
+  }
+  return e;
+}
+
+// Epilogue. Block (i, j), register r of a lane holds row 32 i + 8 (r >> 2) +
+// 4 (l >> 5) + (r & 3) and column 32 j + (l & 31) of the wave sub-tile. The
+// caller has drained every copy and passed a barrier after the last LDS read
+// of the rings.
+template <typename G, int OUT, int MODE>
+__device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&acc)[G::FM][G::FN], char* smem,
+                                            int m0, int n0, int wr, int wc, int wave, int lane, int tid,
+                                            const EpiParams& ep) {
+#pragma clang fp contract(off)
+  float* sa_lds = reinterpret_cast<float*>(smem + G::SC_A);
+  float* sb_lds = reinterpret_cast<float*>(smem + G::SC_B);
+  uint32_t* bias_lds = reinterpret_cast<uint32_t*>(smem + G::SC_BIAS);
+  if constexpr (MODE != EPI_INT) {
+    if (tid < G::BM) sa_lds[tid] = ep.sa;
+    if (tid < G::BN) {
+      sb_lds[tid] = ep.sb;
+      bias_lds[tid] = ep.bias;
+    }
+    __syncthreads();
+  }
+  const bool has_bias = p.bias != nullptr;
+  const int lh = 4 * (lane >> 5);
+  const int lcol = lane & 31;
+  float sb[G::FN], bv[G::FN];
+  static_for<0, G::FN>([&](auto j) {
+    const int c = wc * G::WN + j * 32 + lcol;
+    sb[j] = MODE != EPI_INT ? sb_lds[c] : 0.0f;
+    bv[j] = MODE != EPI_INT ? bias_value(bias_lds[c], p.bias_dtype) : 0.0f;
+  });
+  // Scales of the 4 rows 32 i + 8 q + lh + (0..3): one aligned LDS vector.
+  auto row_scales = [&](int i, int q) -> f32x4 {
+    if constexpr (MODE == EPI_INT) return f32x4{0, 0, 0, 0};
+    else return *reinterpret_cast<const f32x4*>(sa_lds + wr * G::WM + 32 * i + 8 * q + lh);
   };
 
-  // Fragment read offsets of this lane (sub-step h reads logical chunks 4h..4h+3).
-  int a_off[2], b_off[2];
+  constexpr int ES = out_size<OUT>();
+  const bool full = m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((static_cast<int64_t>(p.N) * ES) % 16) == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+  if (full) {
+    // Stage the rounded wave sub-tile in LDS (PF blocks of 32 rows per pass, own
+    // region of the rings per wave), then write whole 16-byte row chunks.
+    constexpr int ROWB = G::WN * ES + 16;                  // padded LDS row pitch
+    constexpr int REGION = G::RING / G::NW;
+    constexpr int PF = (G::FM * 32 * ROWB <= REGION) ? G::FM : (G::FM / 2 * 32 * ROWB <= REGION) ? G::FM / 2 : 1;
+    static_assert(PF * 32 * ROWB <= REGION && G::FM % PF == 0, "epilogue staging does not fit");
+    constexpr int CHUNKS = G::WN * ES / 16;                // 16-byte chunks per row
+    char* region = smem + wave * REGION;
+    char* out = static_cast<char*>(p.out);
+    static_for<0, G::FM / PF>([&](auto pass) {
+      static_for<0, PF>([&](auto ii) {
+        constexpr int i = decltype(pass)::value * PF + decltype(ii)::value;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int lo = (lane & 15) * T::KS + ((((h << 2) | (lane >> 4)) ^ (lane & 7)) << 4);
-    a_off[h] = wr * T::WM * T::KS + lo;
-    b_off[h] = T::STAGE_A + wc * T::WN * T::KS + lo;
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 sa = row_scales(i, q);
+          static_for<0, G::FN>([&](auto j) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t bits = epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias);
+              char* dstp = region + (ii * 32 + 8 * q + lh + e) * ROWB + (j * 32 + lcol) * ES;
+              if constexpr (ES == 4) *reinterpret_cast<uint32_t*>(dstp) = bits;
+              else *reinterpret_cast<uint16_t*>(dstp) = static_cast<uint16_t>(bits);
+            }
+          });
+        }
+      });
+      // LDS accesses of one wave complete in order; the reads below see the writes.
+      constexpr int TOTAL = PF * 32 * CHUNKS;
+      static_assert(TOTAL % 64 == 0, "whole chunk rounds per lane");
+#pragma unroll
+      for (int c0 = 0; c0 < TOTAL; c0 += 64) {
+        const int c = c0 + lane;
+        const int rr = c / CHUNKS, cc = c - rr * CHUNKS;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
+        const int64_t grow = m0 + wr * G::WM + decltype(pass)::value * PF * 32 + rr;
+        const int64_t gcol = n0 + wc * G::WN;
+        *reinterpret_cast<i32x4*>(out + (grow * p.N + gcol) * ES + cc * 16) = v;
+      }
+    });
+  } else {
+    const int row0 = m0 + wr * G::WM + lh;
+    const int col0 = n0 + wc * G::WN + lcol;
+    static_for<0, G::FM>([&](auto i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 sa = row_scales(i, q);
+        static_for<0, G::FN>([&](auto j) {
+          const int col = col0 + j * 32;
+          if (col < p.N) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int row = row0 + 32 * i + 8 * q + e;
+              if (row < p.M)
+                store_elem<OUT>(p.out, static_cast<int64_t>(row) * p.N + col,
+                                epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias));
+            }
+          }
+        });
+      }
+    });
+  }
+}
+
+// 4 waves (2 x 2, one per SIMD), the whole next stage staged in registers.
+template <typename G, int WPE, int OUT, int MODE>
+__global__ __launch_bounds__(G::THREADS, WPE) void k_i8_gemm(I8GemmArgs p) {
+#pragma clang fp contract(off)
+  static_assert(G::NW == 4, "register-staged pipeline: 4 waves");
+  constexpr int NA = G::NA;
+  constexpr int READS = G::KT * (G::FM + G::FN);     // fragment reads per stage
+  constexpr int GROUPS = G::KT / 2 * G::FM;          // MFMA groups (FN each) per half stage
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wr = wave >> 1, wc = wave & 1;
+  int m0, n0;
+  tile_origin<G::BM, G::BN>(p, m0, n0);
+  const EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
+
+  const CopyPlan<4> ca(m0, wave, lane), cw(n0, wave, lane);
+  const uint32_t smem_base = lds_addr_of(smem);
+  const int S = p.K / G::KS;
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  const char* w_base = reinterpret_cast<const char*>(p.w);
+  // A stage s lives in A slot s % NA and W slot s % 2.
+  auto dma_a = [&](auto i_c, int s) {
+    ca.template copy<decltype(i_c)::value>(a_base, p.a_sm, p.M, s,
+                                           smem_base + (NA == 2 ? (s & 1) : s % 3) * G::STAGE_A, wave);
+  };
+  auto dma_w = [&](auto i_c, int s) {
+    cw.template copy<decltype(i_c)::value>(w_base, p.w_sn, p.N, s,
+                                           smem_base + G::RING_B + (s & 1) * G::STAGE_B, wave);
+  };
+  auto dma_stage = [&](int s) {
+    static_for<0, G::A_SEGS>([&](auto i) { dma_a(i, s); });
+    static_for<0, G::B_SEGS>([&](auto i) { dma_w(i, s); });
+  };
+
+  int a_off[G::KT], b_off[G::KT];
+#pragma unroll
+  for (int t = 0; t < G::KT; ++t) {
+    a_off[t] = wr * G::WM * G::KS + frag_offset(t, lane);
+    b_off[t] = G::RING_B + wc * G::WN * G::KS + frag_offset(t, lane);
   }
 
-  i32x4 acc[T::FM][T::FN];
-  static_for<0, T::FM>([&](auto i) {
-    static_for<0, T::FN>([&](auto j) { acc[i][j] = i32x4{0, 0, 0, 0}; });
+  i32x16 acc[G::FM][G::FN];
+  static_for<0, G::FM>([&](auto i) {
+    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
   });
 
-  // Register copies of two stages: [buffer][sub-step][fragment].
-  i32x4 fa[2][2][T::FM], fb[2][2][T::FN];
+  // Register copies of two stages: [buffer][k-step][block].
+  i32x4 fa[2][G::KT][G::FM], fb[2][G::KT][G::FN];
+
+  // Read fragment number r (k-step major, A blocks then W blocks) of the stage
+  // held in A slot `abase` and W slot `bbase` (byte offsets from the slot 0
+  // positions) into register buffer `buf`.
+  auto read_frag = [&](auto r_c, auto buf_c, int abase, int bbase) {
+    constexpr int r = decltype(r_c)::value;
+    constexpr int buf = decltype(buf_c)::value;
+    constexpr int t = r / (G::FM + G::FN), f = r % (G::FM + G::FN);
+    if constexpr (f < G::FM)
+      fa[buf][t][f] = *reinterpret_cast<const i32x4*>(smem + abase + a_off[t] + f * 32 * G::KS);
+    else
+      fb[buf][t][f - G::FM] = *reinterpret_cast<const i32x4*>(smem + bbase + b_off[t] + (f - G::FM) * 32 * G::KS);
+  };
 
   if (S > 0) {
     // ---- prologue: stages 0 and 1 in flight, stage 0 into registers, stage 2
-    // into the freed slot ------------------------------------------------------
-    static_for<0, T::SPW>([&](auto i) { dma(i, 0); });
+    // into the freed slots -----------------------------------------------------
+    dma_stage(0);
     if (S > 1) {
-      static_for<0, T::SPW>([&](auto i) { dma(i, 1); });
-      wait_vm_barrier<T::SPW>();
+      dma_stage(1);
+      wait_vm_barrier<G::SPW>();
     } else {
       wait_vm_barrier<0>();
     }
-    static_for<0, 2>([&](auto h) {
-      static_for<0, T::FM>([&](auto i) {
-        fa[0][h][i] = *reinterpret_cast<const i32x4*>(smem + a_off[h] + i * 16 * T::KS);
-      });
-      static_for<0, T::FN>([&](auto j) {
-        fb[0][h][j] = *reinterpret_cast<const i32x4*>(smem + b_off[h] + j * 16 * T::KS);
-      });
-    });
+    static_for<0, READS>([&](auto r) { read_frag(r, std::integral_constant<int, 0>{}, 0, 0); });
     wait_lds_barrier();
-    static_for<0, T::SPW>([&](auto i) { dma(i, min(2, S - 1)); });
+    dma_stage(min(2, S - 1));
 
     // ---- steady state, two stages per trip so register buffers are static ----
-    //  barrier A  : stage s+1 landed everywhere
-    //  first half : MFMAs of (s, sub-step 0); read all of stage s+1
-    //  barrier B  : every wave holds stage s+1; its slot takes stage s+3
-    //  second half: MFMAs of (s, sub-step 1) with the refill copies between them
-    // Stages s+2 and s+3 are in flight behind the second half. Past the end the
-    // last stage is re-copied into the free slot (never read) so that no branch
-    // splits the MFMA chain, and next-stage reads run unconditionally on a
-    // valid slot (their values are dead after the last stage).
+    //  barrier A  : stage s+1 landed everywhere (copies of stages s+1 and s+2
+    //               are in flight here, in that order, so vmcnt(SPW) leaves
+    //               only the newer)
+    //  first half : MFMAs of k-steps 0..KT/2-1 of stage s; read all of stage
+    //               s+1; with a 3-slot A ring, copy A of stage s+3 into the
+    //               slot that stage s left (read before the previous barrier B)
+    //  barrier B  : every wave holds stage s+1; its W slot (and, with a 2-slot
+    //               A ring, its A slot) takes stage s+3
+    //  second half: MFMAs of k-steps KT/2..KT-1 with the remaining copies
     auto stage = [&](int s, auto cur_c) {
       constexpr int cur = decltype(cur_c)::value;
       constexpr int nxt = cur ^ 1;
-      if (s + 2 < S) wait_vm_barrier<T::SPW>();
-      else wait_vm_barrier<0>();
-      const char* nbase = smem + ((s + 1) & 1) * T::STAGE;
-      static_for<0, T::FM>([&](auto i) {
-        static_for<0, T::FN>([&](auto j) {
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[cur][0][i], fb[cur][0][j], acc[i][j], 0, 0, 0);
+      wait_vm_barrier<G::SPW>();
+      const int abase = (NA == 2 ? ((s + 1) & 1) : (s + 1) % 3) * G::STAGE_A;
+      const int bbase = ((s + 1) & 1) * G::STAGE_B;
+      const int refill_stage = min(s + 3, S - 1);
+      static_for<0, GROUPS>([&](auto g) {
+        constexpr int t = g / G::FM, i = g % G::FM;
+        static_for<0, G::FN>([&](auto j) {
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[cur][t][i], fb[cur][t][j], acc[i][j], 0, 0, 0);
         });
         __builtin_amdgcn_sched_barrier(0);
-        fa[nxt][0][i] = *reinterpret_cast<const i32x4*>(nbase + a_off[0] + i * 16 * T::KS);
-        fa[nxt][1][i] = *reinterpret_cast<const i32x4*>(nbase + a_off[1] + i * 16 * T::KS);
-        if constexpr (i + 2 < T::FN) {
-          fb[nxt][0][i] = *reinterpret_cast<const i32x4*>(nbase + b_off[0] + i * 16 * T::KS);
-          fb[nxt][1][i] = *reinterpret_cast<const i32x4*>(nbase + b_off[1] + i * 16 * T::KS);
+        constexpr int r0 = g * READS / GROUPS, r1 = (g + 1) * READS / GROUPS;
+        static_for<r0, r1>([&](auto r) { read_frag(r, std::integral_constant<int, nxt>{}, abase, bbase); });
+        if constexpr (NA == 3) {
+          constexpr int d0 = g * G::A_SEGS / GROUPS, d1 = (g + 1) * G::A_SEGS / GROUPS;
+          static_for<d0, d1>([&](auto d) { dma_a(d, refill_stage); });
         }
-      });
-      static_for<(T::FN >= 2 ? T::FN - 2 : 0), T::FN>([&](auto j) {
-        fb[nxt][0][j] = *reinterpret_cast<const i32x4*>(nbase + b_off[0] + j * 16 * T::KS);
-        fb[nxt][1][j] = *reinterpret_cast<const i32x4*>(nbase + b_off[1] + j * 16 * T::KS);
+        __builtin_amdgcn_sched_barrier(0);
       });
       wait_lds_barrier();
-      const int refill_stage = min(s + 3, S - 1);
-      static_for<0, T::FM>([&](auto i) {
-        if constexpr (2 * i < T::SPW) dma(std::integral_constant<int, 2 * i>{}, refill_stage);
-        if constexpr (2 * i + 1 < T::SPW) dma(std::integral_constant<int, 2 * i + 1>{}, refill_stage);
-        static_for<0, T::FN>([&](auto j) {
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[cur][1][i], fb[cur][1][j], acc[i][j], 0, 0, 0);
+      constexpr int LATE = (NA == 3 ? 0 : G::A_SEGS) + G::B_SEGS;  // copies after barrier B
+      static_for<0, GROUPS>([&](auto g) {
+        constexpr int t = G::KT / 2 + g / G::FM, i = g % G::FM;
+        constexpr int d0 = g * LATE / GROUPS, d1 = (g + 1) * LATE / GROUPS;
+        static_for<d0, d1>([&](auto d) {
+          constexpr int di = decltype(d)::value;
+          if constexpr (NA == 3) dma_w(d, refill_stage);
+          else if constexpr (di < G::A_SEGS) dma_a(d, refill_stage);
+          else dma_w(std::integral_constant<int, di - G::A_SEGS>{}, refill_stage);
         });
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, G::FN>([&](auto j) {
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[cur][t][i], fb[cur][t][j], acc[i][j], 0, 0, 0);
+        });
+        __builtin_amdgcn_sched_barrier(0);
       });
     };
     int s = 0;
@@ -263,110 +455,133 @@ __global__ __launch_bounds__(256, WPE) void k_i8_gemm(I8GemmArgs p) {
     if (s < S) stage(s, std::integral_constant<int, 0>{});
   }
 
-  // ---- epilogue -------------------------------------------------------------
-  // Lane holds rows 4*(lane>>4)+r, column lane&15 of each 16x16 fragment.
-  const int row0 = m0 + wr * T::WM + 4 * (lane >> 4);
-  const int col0 = n0 + wc * T::WN + (lane & 15);
-  const bool has_bias = p.bias != nullptr;
-  float sa[T::FM][4], sb[T::FN], bv[T::FN];
-  static_for<0, T::FM>([&](auto i) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row0 + i * 16 + r;
-      sa[i][r] = (MODE != EPI_INT && row < p.M) ? p.a_scale[row] : 0.0f;
-    }
-  });
-  static_for<0, T::FN>([&](auto j) {
-    const int col = col0 + j * 16;
-    const bool ok = MODE != EPI_INT && col < p.N;
-    sb[j] = ok ? p.b_scale[p.b_scalar ? 0 : col] : 0.0f;
-    bv[j] = (ok && has_bias) ? load_bias(p.bias, p.bias_dtype, col) : 0.0f;
-  });
-
-  constexpr int ES = out_size<OUT>();
-  const bool full = m0 + BM <= p.M && n0 + BN <= p.N && ((static_cast<int64_t>(p.N) * ES) % 16) == 0 &&
-                    (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
-  if (full) {
-    // Stage the rounded wave sub-tile in LDS (PF fragment rows per pass, own
-    // region per wave), then write whole 16-byte row chunks.
-    constexpr int ROWB = T::WN * ES + 16;                  // padded LDS row pitch
-    constexpr int REGION = T::LDS_BYTES / 4;
-    constexpr int PF = (T::FM * 16 * ROWB <= REGION) ? T::FM : T::FM / 2;
-    static_assert(PF * 16 * ROWB <= REGION && T::FM % PF == 0, "epilogue staging does not fit");
-    constexpr int CHUNKS = T::WN * ES / 16;                // 16-byte chunks per row
-    char* region = smem + wave * REGION;
-    const int lrow = 4 * (lane >> 4);
-    const int lcol = (lane & 15) * ES;
-    char* out = static_cast<char*>(p.out);
-    wait_vm_barrier<0>();  // no copy into LDS in flight; every wave is done reading the ring
-    static_for<0, T::FM / PF>([&](auto pass) {
-      static_for<0, PF>([&](auto ii) {
-        constexpr int i = decltype(pass)::value * PF + decltype(ii)::value;
-        static_for<0, T::FN>([&](auto j) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t bits = epi_bits<OUT, MODE>(acc[i][j][r], sa[i][r], sb[j], bv[j], has_bias);
-            char* dstp = region + (ii * 16 + lrow + r) * ROWB + j * 16 * ES + lcol;
-            if constexpr (ES == 4) *reinterpret_cast<uint32_t*>(dstp) = bits;
-            else *reinterpret_cast<uint16_t*>(dstp) = static_cast<uint16_t>(bits);
-          }
-        });
-      });
-      // LDS accesses of one wave complete in order; the reads below see the writes.
-      constexpr int TOTAL = PF * 16 * CHUNKS;
-      static_assert(TOTAL % 64 == 0, "whole chunk rounds per lane");
-#pragma unroll
-      for (int c0 = 0; c0 < TOTAL; c0 += 64) {
-        const int c = c0 + lane;
-        const int rr = c / CHUNKS, cc = c - rr * CHUNKS;
-        const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
-        const int64_t grow = m0 + wr * T::WM + decltype(pass)::value * PF * 16 + rr;
-        const int64_t gcol = n0 + wc * T::WN;
-        *reinterpret_cast<i32x4*>(out + (grow * p.N + gcol) * ES + cc * 16) = v;
-      }
-    });
-  } else {
-    static_for<0, T::FN>([&](auto j) {
-      const int col = col0 + j * 16;
-      if (col < p.N) {
-        static_for<0, T::FM>([&](auto i) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = row0 + i * 16 + r;
-            if (row < p.M)
-              store_elem<OUT>(p.out, static_cast<int64_t>(row) * p.N + col,
-                              epi_bits<OUT, MODE>(acc[i][j][r], sa[i][r], sb[j], bv[j], has_bias));
-          }
-        });
-      }
-    });
-  }
+  wait_vm_barrier<0>();  // no copy into LDS in flight; every wave is done reading the rings
+  i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
 }
 
-template <int BM, int BN, int WPE, int OUT, int MODE>
+// 8 waves (WGM x WGN with WGN = 2, two per SIMD), fragments read from LDS one
+// k-step ahead, one barrier per stage:
+//   barrier    : A and W of stage s landed everywhere (the newest copy group,
+//                A of stage s+1, may still be in flight: vmcnt(A_SEGS)), and
+//                every wave is done with stage s-1's slots
+//   copies     : W of stage s+1 into the W slot of stage s-1, then A of stage
+//                s+2 into the A slot of stage s-1, spread over the k-steps
+//   k-steps    : read k-step t+1's fragments, MFMAs of k-step t
+template <typename G, int OUT, int MODE>
+__global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_jit(I8GemmArgs p) {
+#pragma clang fp contract(off)
+  static_assert(G::NA == 3, "JIT pipeline keeps A two stages ahead");
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+  int m0, n0;
+  tile_origin<G::BM, G::BN>(p, m0, n0);
+  const EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
+
+  const CopyPlan<G::NW> ca(m0, wave, lane), cw(n0, wave, lane);
+  const uint32_t smem_base = lds_addr_of(smem);
+  const int S = p.K / G::KS;
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  const char* w_base = reinterpret_cast<const char*>(p.w);
+  auto dma_a = [&](auto i_c, int s) {
+    ca.template copy<decltype(i_c)::value>(a_base, p.a_sm, p.M, s, smem_base + (s % 3) * G::STAGE_A, wave);
+  };
+  auto dma_w = [&](auto i_c, int s) {
+    cw.template copy<decltype(i_c)::value>(w_base, p.w_sn, p.N, s, smem_base + G::RING_B + (s & 1) * G::STAGE_B,
+                                           wave);
+  };
+
+  int a_off[G::KT], b_off[G::KT];
+#pragma unroll
+  for (int t = 0; t < G::KT; ++t) {
+    a_off[t] = wr * G::WM * G::KS + frag_offset(t, lane);
+    b_off[t] = G::RING_B + wc * G::WN * G::KS + frag_offset(t, lane);
+  }
+
+  i32x16 acc[G::FM][G::FN];
+  static_for<0, G::FM>([&](auto i) {
+    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
+  });
+  i32x4 fa[2][G::FM], fb[2][G::FN];  // [k-step parity][block]
+
+  auto read_step = [&](auto t_c, auto buf_c, int abase, int bbase) {
+    constexpr int t = decltype(t_c)::value, buf = decltype(buf_c)::value;
+    static_for<0, G::FM>([&](auto i) {
+      fa[buf][i] = *reinterpret_cast<const i32x4*>(smem + abase + a_off[t] + i * 32 * G::KS);
+    });
+    static_for<0, G::FN>([&](auto j) {
+      fb[buf][j] = *reinterpret_cast<const i32x4*>(smem + bbase + b_off[t] + j * 32 * G::KS);
+    });
+  };
+
+  if (S > 0) {
+    // prologue: A(0), W(0), A(1) in flight
+    static_for<0, G::A_SEGS>([&](auto i) { dma_a(i, 0); });
+    static_for<0, G::B_SEGS>([&](auto i) { dma_w(i, 0); });
+    static_for<0, G::A_SEGS>([&](auto i) { dma_a(i, min(1, S - 1)); });
+    constexpr int COPIES = G::A_SEGS + G::B_SEGS;  // per wave and stage, spread over KT k-steps
+    for (int s = 0; s < S; ++s) {
+      wait_vm_barrier<G::A_SEGS>();
+      const int abase = (s % 3) * G::STAGE_A;
+      const int bbase = (s & 1) * G::STAGE_B;
+      const int w_next = min(s + 1, S - 1), a_next = min(s + 2, S - 1);
+      read_step(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, abase, bbase);
+      static_for<0, G::KT>([&](auto t_c) {
+        constexpr int t = decltype(t_c)::value;
+        if constexpr (t + 1 < G::KT)
+          read_step(std::integral_constant<int, t + 1>{}, std::integral_constant<int, (t + 1) & 1>{}, abase, bbase);
+        constexpr int d0 = t * COPIES / G::KT, d1 = (t + 1) * COPIES / G::KT;
+        static_for<d0, d1>([&](auto d) {
+          constexpr int di = decltype(d)::value;
+          if constexpr (di < G::B_SEGS) dma_w(d, w_next);
+          else dma_a(std::integral_constant<int, di - G::B_SEGS>{}, a_next);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, G::FM>([&](auto i) {
+          static_for<0, G::FN>([&](auto j) {
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[t & 1][i], fb[t & 1][j], acc[i][j], 0, 0, 0);
+          });
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    }
+  }
+
+  wait_vm_barrier<0>();  // no copy into LDS in flight; every wave is done reading the rings
+  i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
+}
+
+template <typename G, int WPE, int OUT, int MODE>
 hipError_t launch_tile(const I8GemmArgs& p, hipStream_t stream) {
-  const int blocks = ceil_div(p.M, BM) * ceil_div(p.N, BN);
-  hipLaunchKernelGGL((k_i8_gemm<BM, BN, WPE, OUT, MODE>), dim3(blocks), dim3(256), 0, stream, p);
+  static_assert(G::LDS_BYTES * WPE <= 160 * 1024, "LDS per CU");
+  const int blocks = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
+  if constexpr (G::NW == 4)
+    hipLaunchKernelGGL((k_i8_gemm<G, WPE, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
+  else
+    hipLaunchKernelGGL((k_i8_gemm_jit<G, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WPE, int OUT>
+template <typename G, int WPE, int OUT>
 hipError_t launch_mode(const I8GemmArgs& p, hipStream_t stream) {
   // Orders F and E coincide for fp32 output (no intermediate rounding).
-  if (p.epi & QG_EPI_GELU_TANH) return launch_tile<BM, BN, WPE, OUT, EPI_GELU>(p, stream);
-  if (p.epi & QG_EPI_ORDER_FUSED_FMA) return launch_tile<BM, BN, WPE, OUT, EPI_FMA>(p, stream);
+  if (p.epi & QG_EPI_GELU_TANH) return launch_tile<G, WPE, OUT, EPI_GELU>(p, stream);
+  if (p.epi & QG_EPI_ORDER_FUSED_FMA) return launch_tile<G, WPE, OUT, EPI_FMA>(p, stream);
   if constexpr (OUT != QG_F32) {
-    if (p.epi & QG_EPI_ORDER_EAGER) return launch_tile<BM, BN, WPE, OUT, EPI_EAGER>(p, stream);
+    if (p.epi & QG_EPI_ORDER_EAGER) return launch_tile<G, WPE, OUT, EPI_EAGER>(p, stream);
   }
-  return launch_tile<BM, BN, WPE, OUT, EPI_F>(p, stream);
+  return launch_tile<G, WPE, OUT, EPI_F>(p, stream);
 }
 
-template <int BM, int BN, int WPE>
+template <typename G, int WPE>
 hipError_t launch_variant(const I8GemmArgs& p, hipStream_t stream) {
-  if (p.a_scale == nullptr) return launch_tile<BM, BN, WPE, QG_I32, EPI_INT>(p, stream);
-  if (p.out_dtype == QG_F16) return launch_mode<BM, BN, WPE, QG_F16>(p, stream);
-  if (p.out_dtype == QG_BF16) return launch_mode<BM, BN, WPE, QG_BF16>(p, stream);
-  return launch_mode<BM, BN, WPE, QG_F32>(p, stream);
+  if (p.a_scale == nullptr) return launch_tile<G, WPE, QG_I32, EPI_INT>(p, stream);
+  if (p.out_dtype == QG_F16) return launch_mode<G, WPE, QG_F16>(p, stream);
+  if (p.out_dtype == QG_BF16) return launch_mode<G, WPE, QG_BF16>(p, stream);
+  return launch_mode<G, WPE, QG_F32>(p, stream);
 }
 
 }  // namespace
@@ -377,8 +592,8 @@ hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream) {
   // CUs (4096x3072 -> 256 tiles, x9216 -> 768, x12288 -> 1024). Smaller
   // problems use 128x128 tiles so that more CUs get work.
   const long big = static_cast<long>(ceil_div(p.M, 256)) * ceil_div(p.N, 192);
-  if (big >= 192) return launch_variant<256, 192, 1>(p, stream);
-  return launch_variant<128, 128, 2>(p, stream);
+  if (big >= 192) return launch_variant<I8Geo<256, 192, 4, 2, 3>, 1>(p, stream);
+  return launch_variant<I8Geo<128, 128, 2, 2, 2>, 2>(p, stream);
 }
 
 }  // namespace qg

@@ -1,11 +1,14 @@
 // Per-row dynamic INT8 quantizer and the strided int8 row packer.
 //
-// quant: one wave per row (rows are at most a few tens of KB, so a wave keeps
-// 64 x 16-byte loads in flight and needs no workgroup-level reduction).
-//   pass 1: absmax over the row (16-byte vector loads when the row allows);
+// quant: one wave per row, no workgroup-level reduction.
 //   step = max(absmax / 127, 1e-20)          (IEEE fp32 division)
-//   pass 2: q = clamp(round(x / step), -127, 127) with IEEE division, the row
-//           is re-read from L2 (it was just streamed), so HBM sees it once.
+//   q = clamp(round(x / step), -127, 127)    (round of the IEEE quotient)
+// Rows of up to 24 x 64 16-byte chunks (12288 fp16) are loaded into registers
+// once, all loads in flight together, and quantized from there. The quotient is
+// formed as x * rcp(step) (a few ulps from x / step); only when that lands
+// within 2^-12 of a rounding boundary (n + 1/2) is the IEEE division done, so
+// the rounded result is always that of the exact quotient. Longer or strided
+// rows take a two-pass kernel (pass 2 re-reads the row from L2).
 // The step formula and the half-away rounding follow the reference's
 // in-tree quantizer rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:76-92; the
 // half-even mode is the BASELINE per-token rule (absmax/127, round-half-even).
@@ -58,6 +61,87 @@ __device__ __forceinline__ int quant_one(float x, float step) {
   }
   q = fminf(fmaxf(q, -127.0f), 127.0f);
   return static_cast<int>(q);
+}
+
+// Fast rounding of z = x * rstep (relative error below 1.5 * 2^-23, i.e. below
+// 2^-15.5 for |z| < 128): clamp to +-127, then adding 1.5 * 2^23 rounds to the
+// nearest integer n, whose two's-complement byte is the low byte of the sum's
+// bits. n is the rounded exact quotient, in both modes, unless z lies within
+// 2^-13 of a half-integer (|z - n| > 1/2 - 2^-13); such chunks are redone with
+// the IEEE quotient.
+constexpr float kRoundMagic = 12582912.0f;            // 1.5 * 2^23
+constexpr float kRiskyDist = 0.5f - 0.0001220703125f;  // 1/2 - 2^-13
+
+// Register-resident rows: lane l holds chunks l + 64 i, i < NCH.
+template <int XT, int MODE, int NCH>
+__global__ __launch_bounds__(256) void k_quant_rows_reg(const char* x, int64_t x_sm, int M, int K, int8_t* q,
+                                                        int64_t q_sm, int k_pad, float* step_out) {
+#pragma clang fp contract(off)
+  constexpr int ES = XType<XT>::size;
+  constexpr int E = 16 / ES;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const char* xr = x + static_cast<int64_t>(row) * x_sm * ES;
+  int8_t* qr = q + static_cast<int64_t>(row) * q_sm;
+  const int chunks = K / E;
+  i32x4 raw[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane + 64 * i;
+    raw[i] = c < chunks ? reinterpret_cast<const i32x4*>(xr)[c] : i32x4{0, 0, 0, 0};
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    float v[E];
+    decode_chunk<XT>(raw[i], v);
+#pragma unroll
+    for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  }
+  amax = wave_max(amax);
+  const float step = fmaxf(amax / 127.0f, 1.0e-20f);
+  const float rstep = __builtin_amdgcn_rcpf(step);
+  // Decode again below rather than keep every decoded element live.
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) asm volatile("" : "+v"(raw[i]));
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane + 64 * i;
+    float v[E];
+    decode_chunk<XT>(raw[i], v);
+    uint32_t b[E];
+    float dmax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float z = v[e] * rstep;
+      const float m = fminf(fmaxf(z, -127.0f), 127.0f) + kRoundMagic;
+      dmax = fmaxf(dmax, fabsf(z - (m - kRoundMagic)));
+      b[e] = __float_as_uint(m);
+    }
+    const bool risky = dmax > kRiskyDist;
+    if (__builtin_expect(__any(risky), 0)) {
+      if (risky) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) b[e] = static_cast<uint32_t>(quant_one<MODE>(v[e], step));
+      }
+    }
+    // low bytes of 4 words -> one word (byte e of the result = byte 0 of b[e])
+    uint32_t packed[E / 4 > 0 ? E / 4 : 1];
+#pragma unroll
+    for (int w = 0; w < E / 4; ++w) {
+      const uint32_t lo = __builtin_amdgcn_perm(b[4 * w + 1], b[4 * w], 0x0c0c0400u);
+      const uint32_t hi = __builtin_amdgcn_perm(b[4 * w + 3], b[4 * w + 2], 0x04000c0cu);
+      packed[w] = lo | hi;
+    }
+    if (c < chunks) {
+      if constexpr (E == 4) reinterpret_cast<uint32_t*>(qr)[c] = packed[0];
+      else if constexpr (E == 8) reinterpret_cast<uint2*>(qr)[c] = make_uint2(packed[0], packed[1]);
+      else reinterpret_cast<uint4*>(qr)[c] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    }
+  }
+  for (int k = K + lane; k < k_pad; k += 64) qr[k] = 0;
+  if (lane == 0) step_out[row] = step;
 }
 
 template <int XT, int MODE, bool VEC>
@@ -121,6 +205,20 @@ hipError_t launch_quant_t(const void* x, int64_t x_sm, int64_t x_sk, int64_t M, 
                    (qa % E) == 0 && (q_sm % E) == 0;
   const dim3 grid(static_cast<unsigned>(ceil_div<int64_t>(M, 4)));
   const char* xp = static_cast<const char*>(x);
+  const int64_t per_lane = ceil_div<int64_t>(K / E, 64);  // 16-byte chunks per lane
+  const int m = static_cast<int>(M), k = static_cast<int>(K), kp = static_cast<int>(k_pad);
+  constexpr int kMaxReg = ES == 1 ? 12 : 24;  // 16-byte chunks per lane held in registers
+  if (vec && per_lane <= kMaxReg) {
+    if (per_lane <= 4)
+      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 4>), grid, dim3(256), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
+    else if (per_lane <= 8)
+      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 8>), grid, dim3(256), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
+    else if (per_lane <= 12)
+      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 12>), grid, dim3(256), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
+    else if constexpr (kMaxReg == 24)
+      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 24>), grid, dim3(256), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
+    return hipGetLastError();
+  }
   if (vec)
     hipLaunchKernelGGL((k_quant_rows<XT, MODE, true>), grid, dim3(256), 0, stream, xp, x_sm, x_sk,
                        static_cast<int>(M), static_cast<int>(K), q, q_sm, static_cast<int>(k_pad), step);

@@ -60,6 +60,48 @@ def test_quant_rows_random(cuda, dtype, shape):
     assert np.array_equal(q2.cpu().numpy(), qo)
 
 
+def _near_tie_rows(dtype, m, k, seed):
+    """Rows whose quotients x / step sit on and around the rounding boundaries
+    n + 1/2 (exact ties, a few ulps off, and at the edge of the quantizer's
+    2^-12 fast-path band), each row's absmax placed in column 0."""
+    rng = np.random.default_rng(seed)
+    rows = np.zeros((m, k), np.float64)
+    deltas = np.array([0.0, 1e-7, -1e-7, 3e-7, -3e-7, 1e-6, -1e-6, 1e-5, -1e-5, 2.3e-4, -2.3e-4,
+                       2.5e-4, -2.5e-4, 1e-3, -1e-3, 0.25, -0.25])
+    for r in range(m):
+        a = torch.tensor(float(rng.uniform(0.5, 100.0))).to(dtype).double().item()
+        step = float(np.float32(np.float32(a) / np.float32(127.0)))
+        n = rng.integers(-126, 126, k)
+        d = deltas[rng.integers(0, len(deltas), k)]
+        x = (n + 0.5 + d) * step
+        x = torch.from_numpy(x).to(dtype).double().numpy()
+        x = np.clip(x, -a, a)
+        x[0] = a
+        rows[r] = x
+    return torch.from_numpy(rows).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("k", [4096, 20480])
+def test_quant_rows_near_ties(cuda, dtype, k):
+    """Bit-exact rounding of x / step at and next to half-integers, in the
+    register-resident kernel (k = 4096) and the two-pass kernel (k = 20480)."""
+    from rdna2_ops.quantize import quantize_int8_rowwise
+    x = _near_tie_rows(dtype, 48, k, seed=k + 3)
+    xf = x.float().numpy()
+    _, so = o.quant_rows(xf, "half_even")
+    z = xf.astype(np.float64) / so[:, None].astype(np.float64)
+    band = np.abs(z - np.floor(z) - 0.5) < 2.0 ** -12
+    if dtype == torch.float32:
+        assert band.sum() > 1000  # the exact-division fallback is exercised
+    for rounding in ("half_even", "half_away"):
+        case(f"quant near ties {dtype} k{k} {rounding}")
+        q, step = quantize_int8_rowwise(x.to(cuda), rounding=rounding)
+        qo, so = o.quant_rows(xf, rounding)
+        assert np.array_equal(step.cpu().numpy().reshape(-1), so)
+        assert np.array_equal(q.cpu().numpy(), qo), (q.cpu().numpy() != qo).sum()
+
+
 @pytest.mark.parametrize("layout", ["weight_nk", "rhs_kn"])
 @pytest.mark.parametrize("scalar", [False, True])
 def test_int8_small_checks_golden(cuda, layout, scalar):

@@ -554,12 +554,139 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_jit(I8GemmArgs p) {
   i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
 }
 
+// 8 waves in two groups that share the SIMDs pairwise (waves w and w + 4) and
+// alternate roles every half stage ("ping-pong"): while one wave of a SIMD
+// issues its whole stage of MFMAs back to back, the other reads its next
+// fragments from LDS and issues copies, so a wave waiting on a copy or an LDS
+// read never leaves the MFMA pipe idle. Group X (waves 0-3) copies W, group Y
+// (waves 4-7) copies A. Phases of stage s:
+//   B0(s)  barrier: every wave is done with stage s-1's data
+//   P1(s)  X: MFMAs of stage s (fragments read in P2(s-1))
+//          Y: read stage s, copy A of stage s+2 into the A slot of stage s-1
+//   B1(s)  X: W(s+1) landed (its newest copies), Y: A(s+1) landed (only
+//          A(s+2) may still fly) and Y's reads of stage s are complete
+//   P2(s)  X: read stage s+1, copy W of stage s+2 into the W slot of stage s
+//          Y: MFMAs of stage s
+constexpr bool kI8PingPong = true;
+
+template <typename G, int OUT, int MODE>
+__global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
+#pragma clang fp contract(off)
+  static_assert(G::NW == 8 && G::NA == 3 && G::KT == 4, "ping-pong geometry");
+  constexpr int XS = G::BN / 32, YS = G::BM / 32;  // copies per wave and stage (W by X, A by Y)
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+  const bool grp_x = wave < 4;
+  const int gw = wave & 3;
+  int m0, n0;
+  tile_origin<G::BM, G::BN>(p, m0, n0);
+  const EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
+
+  const CopyPlan<4> plan(grp_x ? n0 : m0, gw, lane);
+  const uint32_t smem_base = lds_addr_of(smem);
+  const int S = p.K / G::KS;
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  const char* w_base = reinterpret_cast<const char*>(p.w);
+  auto copy_w = [&](auto i_c, int s) {
+    plan.template copy<decltype(i_c)::value>(w_base, p.w_sn, p.N, s, smem_base + G::RING_B + (s & 1) * G::STAGE_B, gw);
+  };
+  auto copy_a = [&](auto i_c, int s) {
+    plan.template copy<decltype(i_c)::value>(a_base, p.a_sm, p.M, s, smem_base + (s % 3) * G::STAGE_A, gw);
+  };
+
+  int a_off[G::KT], b_off[G::KT];
+#pragma unroll
+  for (int t = 0; t < G::KT; ++t) {
+    a_off[t] = wr * G::WM * G::KS + frag_offset(t, lane);
+    b_off[t] = G::RING_B + wc * G::WN * G::KS + frag_offset(t, lane);
+  }
+
+  i32x16 acc[G::FM][G::FN];
+  static_for<0, G::FM>([&](auto i) {
+    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
+  });
+  i32x4 fa[G::KT][G::FM], fb[G::KT][G::FN];
+
+  // Read stage s into the fragment registers with this wave's copies of stage
+  // cs spread between the k-steps (W copies for X, A copies for Y).
+  auto load_phase = [&](auto x_c, int s, int cs) {
+    constexpr bool X = decltype(x_c)::value;
+    const int abase = (s % 3) * G::STAGE_A;
+    const int bbase = (s & 1) * G::STAGE_B;
+    static_for<0, G::KT>([&](auto t_c) {
+      constexpr int t = decltype(t_c)::value;
+      static_for<0, G::FM>([&](auto i) {
+        fa[t][i] = *reinterpret_cast<const i32x4*>(smem + abase + a_off[t] + i * 32 * G::KS);
+      });
+      static_for<0, G::FN>([&](auto j) {
+        fb[t][j] = *reinterpret_cast<const i32x4*>(smem + bbase + b_off[t] + j * 32 * G::KS);
+      });
+      if constexpr (X) {
+        static_for<t * XS / G::KT, (t + 1) * XS / G::KT>([&](auto d) { copy_w(d, cs); });
+      } else {
+        static_for<t * YS / G::KT, (t + 1) * YS / G::KT>([&](auto d) { copy_a(d, cs); });
+      }
+    });
+  };
+  auto mfma_phase = [&]() {
+    __builtin_amdgcn_s_setprio(1);
+    static_for<0, G::KT>([&](auto t) {
+      static_for<0, G::FM>([&](auto i) {
+        static_for<0, G::FN>([&](auto j) {
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[t][i], fb[t][j], acc[i][j], 0, 0, 0);
+        });
+      });
+    });
+    __builtin_amdgcn_s_setprio(0);
+  };
+  using XT_ = std::true_type;
+  using YT_ = std::false_type;
+
+  // Both groups pass the same barriers: one before the prologue, then B0 and
+  // B1 of every stage.
+  if (S > 0) {
+    if (grp_x) {
+      // prologue: W(0) landed everywhere, then read stage 0 and copy W(1)
+      static_for<0, XS>([&](auto d) { copy_w(d, 0); });
+      wait_vm<0>();
+      __builtin_amdgcn_s_barrier();
+      load_phase(XT_{}, 0, min(1, S - 1));
+      for (int s = 0; s < S; ++s) {
+        __builtin_amdgcn_s_barrier();  // B0(s)
+        mfma_phase();
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1(s)
+        load_phase(XT_{}, min(s + 1, S - 1), min(s + 2, S - 1));
+      }
+    } else {
+      static_for<0, YS>([&](auto d) { copy_a(d, 0); });
+      static_for<0, YS>([&](auto d) { copy_a(d, min(1, S - 1)); });
+      wait_vm<YS>();
+      __builtin_amdgcn_s_barrier();
+      for (int s = 0; s < S; ++s) {
+        __builtin_amdgcn_s_barrier();  // B0(s)
+        load_phase(YT_{}, s, min(s + 2, S - 1));
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(YS) : "memory");  // B1(s)
+        mfma_phase();
+      }
+    }
+  }
+
+  wait_vm_barrier<0>();  // no copy into LDS in flight; every wave is done reading the rings
+  i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
+}
+
 template <typename G, int WPE, int OUT, int MODE>
 hipError_t launch_tile(const I8GemmArgs& p, hipStream_t stream) {
   static_assert(G::LDS_BYTES * WPE <= 160 * 1024, "LDS per CU");
   const int blocks = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
   if constexpr (G::NW == 4)
     hipLaunchKernelGGL((k_i8_gemm<G, WPE, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
+  else if (kI8PingPong)
+    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
   else
     hipLaunchKernelGGL((k_i8_gemm_jit<G, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
   return hipGetLastError();

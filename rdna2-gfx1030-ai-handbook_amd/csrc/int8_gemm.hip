@@ -75,17 +75,17 @@ struct I8Geo {
 
 __device__ __forceinline__ float gelu_tanh(float x) {
 #pragma clang fp contract(off)
-  // 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), in the operation
-  // order of ATen's CPU GeluKernel (tanh approximation). tanh(u) is evaluated
-  // as 1 - 2 / (exp(2u) + 1) with the hardware exp2 and reciprocal: absolute
-  // error a few 1e-7, far below one fp16/bf16 ulp of the result.
-  const float kBeta = 0.7978845608028654f;
-  const float kKappa = 0.044715f;
-  const float x_cube = x * x * x;
-  const float inner = kBeta * (x + kKappa * x_cube);
-  const float e = __builtin_amdgcn_exp2f(inner * 2.8853900817779268f);  // exp(2u) = 2^(2u log2 e)
-  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-  return 0.5f * x * (1.0f + t);
+  // 0.5 * x * (1 + tanh(u)), u = sqrt(2/pi) * (x + 0.044715 * x^3): the
+  // tanh approximation of ATen's CPU GeluKernel, evaluated as the identical
+  // x * sigmoid(2u) = x / (1 + 2^(-2u log2 e)) with 2u log2 e = x (c0 + c1 x^2),
+  // the hardware exp2 and reciprocal. Absolute error a few 1e-7, far below
+  // one fp16/bf16 ulp of the result; large +x gives x, large -x gives -0 and
+  // -inf gives NaN, as the reference formula does.
+  const float c0 = 2.3022082f;   // 2 sqrt(2/pi) log2(e)
+  const float c1 = 0.10294324f;  // c0 * 0.044715
+  const float p = __builtin_fmaf(c1, x * x, c0);
+  const float e = __builtin_amdgcn_exp2f(-(x * p));
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // Raw storage bits of bias[col] (fp32, fp16 or bf16) and their fp32 value.
@@ -586,16 +586,30 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
   tile_origin<G::BM, G::BN>(p, m0, n0);
   const EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
 
+  // Copy i of a wave covers rows 8 (gw + 4 i) .. + 7 of its operand's tile;
+  // the 32-bit row offsets (clamped rows, swizzled chunk) are computed once.
   const CopyPlan<4> plan(grp_x ? n0 : m0, gw, lane);
   const uint32_t smem_base = lds_addr_of(smem);
   const int S = p.K / G::KS;
   const char* a_base = reinterpret_cast<const char*>(p.a);
   const char* w_base = reinterpret_cast<const char*>(p.w);
+  uint32_t voff[YS];
+  {
+    const int rows = grp_x ? p.N : p.M;
+    const uint32_t stride = static_cast<uint32_t>(grp_x ? p.w_sn : p.a_sm);
+    static_for<0, YS>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, rows - 1)) * stride + plan.chunk16;
+    });
+  }
   auto copy_w = [&](auto i_c, int s) {
-    plan.template copy<decltype(i_c)::value>(w_base, p.w_sn, p.N, s, smem_base + G::RING_B + (s & 1) * G::STAGE_B, gw);
+    constexpr int I = decltype(i_c)::value;
+    dma16s(w_base + static_cast<int64_t>(s) * G::KS, voff[I],
+           smem_base + G::RING_B + (s & 1) * G::STAGE_B + (gw + 4 * I) * 1024);
   };
   auto copy_a = [&](auto i_c, int s) {
-    plan.template copy<decltype(i_c)::value>(a_base, p.a_sm, p.M, s, smem_base + (s % 3) * G::STAGE_A, gw);
+    constexpr int I = decltype(i_c)::value;
+    dma16s(a_base + static_cast<int64_t>(s) * G::KS, voff[I], smem_base + (s % 3) * G::STAGE_A + (gw + 4 * I) * 1024);
   };
 
   int a_off[G::KT], b_off[G::KT];

@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=("w4a16", "fp8"), default=None,
+    ap.add_argument("--only", choices=("w4a16", "fp8", "moe"), default=None,
                     help="run one secondary measurement alone and print it (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -228,6 +228,38 @@ def run_fp8(torch, lib, _lib, dev):
     return res
 
 
+def run_moe(torch, dev, iters=20):
+    """Secondary: BASELINE configuration 4, MoE prefill (4096 tokens, top-8 of 64
+    experts, hidden 2048, F 768) through rdna2_ops.moe_int8: routing, dispatch,
+    x quantization, grouped gate/up GEMM + SiLU*mul, h quantization, grouped
+    down GEMM * routing weight, combine. Ops count the routed rows only
+    (309.2 G, no padding); bytes are the algorithmic ~487 MB (weights once,
+    int8 activations, bf16 h written and read, bf16 out)."""
+    from rdna2_ops import moe_int8, synthetic
+    c = synthetic.cfg4()
+    prep = moe_int8.prepare_moe_weights(c.w_gate.to(dev), c.w_up.to(dev), c.w_down.to(dev))
+    x, lg = c.x.to(dev), c.logits.to(dev)
+    for _ in range(3):
+        moe_int8.moe_int8_forward(x, lg, prep, top_k=c.top_k)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(iters):
+        moe_int8.moe_int8_forward(x, lg, prep, top_k=c.top_k)
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    t, h = c.x.shape
+    e, f = c.w_gate.shape[0], c.w_gate.shape[1]
+    ops = 2.0 * t * c.top_k * (h * 2 * f + f * h)
+    nbytes = e * 3 * f * h + t * h * 2 + t * c.top_k * h + 2 * (t * c.top_k * f * 2) + t * h * 2
+    tops = ops / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 1), "TOPS": round(tops, 1), "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4),
+            "GBs_algorithmic": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "ops": ops, "bytes": nbytes}
+
+
 def traffic_bytes(name="int8_gemm_cfg1_chain_traffic.json"):
     """HBM bytes per launch of a kernel, measured with rocprofv3 --pmc
     FETCH_SIZE / WRITE_SIZE (scaled by a plain-copy calibration) and recorded in
@@ -263,7 +295,9 @@ def main():
         return
     lib = _lib.library()
     if args.only:
-        res = run_w4a16(torch, lib, _lib, dev) if args.only == "w4a16" else run_fp8(torch, lib, _lib, dev)
+        runs = {"w4a16": lambda: run_w4a16(torch, lib, _lib, dev), "fp8": lambda: run_fp8(torch, lib, _lib, dev),
+                "moe": lambda: run_moe(torch, dev)}
+        res = runs[args.only]()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return
     chain = Chain(torch, lib, _lib, quantize_int8_rowwise, synthetic.cfg1(), dev)
@@ -325,6 +359,7 @@ def main():
         sec["w4a16_m16"] = w4[16]
         sec["w4a16_prefill_m2048"] = w4[2048]
         sec["fp8_cfg3"] = run_fp8(torch, lib, _lib, dev)
+        sec["moe_cfg4"] = run_moe(torch, dev)
         line["secondary"] = sec
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import time_cfg1_chain

@@ -237,6 +237,79 @@ int qg_fp8w_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_sk, int64_t
                  int bias_dtype, void* out, int out_dtype, void* workspace,
                  size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * MoE prefill with grouped INT8 GEMMs.
+ * No counterpart in the reference repository (it has no MoE kernel); the
+ * stages follow BASELINE's CPU formulation: softmax + top-k routing, tokens
+ * sorted and padded per expert, per-expert INT8 GEMMs with a SiLU * mul
+ * epilogue, scatter-add with the routing weights.
+ * ------------------------------------------------------------------------- */
+
+/* Routed rows per grouped-GEMM tile (the dispatch builds its tile table in
+ * units of this many rows). */
+#define QG_MOE_TILE_ROWS 192
+
+/* int32 words of the dispatch's counts workspace per expert. */
+#define QG_MOE_COUNTS_PER_EXPERT 259
+
+/* Epilogues of qg_moe_grouped_gemm; v = f32(acc) * (a_scale[row] * b_scale[e, n]). */
+enum qg_moe_epilogue {
+  QG_MOE_EPI_I32 = 0,      /* out int32 [rows, n] = acc */
+  QG_MOE_EPI_SILU_MUL = 1, /* W rows 32b..32b+15 are gate rows and 32b+16..32b+31 the
+                              up rows of features 16b..16b+15:
+                              out bf16 [rows, n / 2] = silu(v_gate) * v_up */
+  QG_MOE_EPI_ROUTE = 2     /* out bf16 [tokens * top_k, n], row row_slot[r]
+                              = v * row_weight[r] */
+};
+
+/* Upper bounds of the routed rows and tiles of a dispatch (sizes of the
+ * row_* and tiles arrays): rows_max = tokens * top_k + n_experts * (pad - 1),
+ * tiles_max = ceil(rows_max / QG_MOE_TILE_ROWS) + n_experts. */
+int qg_moe_sizes(int64_t tokens, int n_experts, int top_k, int pad, int64_t* rows_max, int64_t* tiles_max);
+
+/* Routing and dispatch. logits: fp32 [tokens, n_experts] (row stride l_sm),
+ * n_experts <= 64, 1 <= top_k <= n_experts, pad >= 1.
+ * experts int32 [tokens, top_k]: the top_k experts by logit (descending;
+ *   equal logits: lower index first); weights fp32 [tokens, top_k]: their
+ *   softmax probabilities over all experts (not renormalised).
+ * Routed rows grouped by expert (expert 0 first), each expert's segment
+ * padded to a multiple of pad rows: row_token (token, -1 for padding),
+ * row_weight (0 for padding), row_slot (t * top_k + k, -1 for padding), each
+ * [rows_max]; tokens are in arbitrary order inside a segment.
+ * tiles int32 [tiles_max][4] = {expert (-1: unused), first row, end of the
+ * expert's valid rows, 0}; tiles[0][3] = number of tiles in use (the used
+ * tiles come first). counts: int32 workspace [QG_MOE_COUNTS_PER_EXPERT *
+ * n_experts]: per-expert counts and segment offsets first, then the sort's
+ * per-block histograms. */
+int qg_moe_dispatch(const float* logits, int64_t l_sm, int64_t tokens, int n_experts, int top_k, int pad,
+                    int32_t* experts, float* weights, int32_t* counts, int32_t* row_token,
+                    float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,
+                    int64_t tiles_max, void* stream);
+
+/* Grouped INT8 GEMM over the dispatch's tile table: for each routed row r of
+ * expert e, acc[r, n] = sum_k a[src(r), k] * w[e, n, k] with src(r) =
+ * row_token[r] (row_token NULL: r itself), then the epilogue. a: int8
+ * [a_rows, k] (row stride a_sm); w: int8 [n_experts][n, k] (row stride w_sn,
+ * expert stride w_estride bytes); a_scale fp32 indexed like a's rows;
+ * b_scale fp32 [n_experts, n]. k % 128 == 0, 16-byte aligned rows;
+ * QG_MOE_EPI_SILU_MUL needs n % 32 == 0. out: out_rows rows (>= rows_max, or
+ * tokens * top_k for QG_MOE_EPI_ROUTE) of row stride out_sm (elements). Tile
+ * entries naming an expert >= n_experts or rows outside [0, rows_max) are
+ * skipped, row_token entries are clamped into [0, a_rows) and route rows
+ * outside [0, out_rows) are not written. */
+int qg_moe_grouped_gemm(const int8_t* a, int64_t a_sm, int64_t a_rows, const int32_t* row_token,
+                        int64_t rows_max, int64_t k, const int8_t* w, int64_t w_sn, int64_t w_estride,
+                        int64_t n, int n_experts, const int32_t* tiles, int64_t tiles_max,
+                        const float* a_scale, const float* b_scale, const float* row_weight,
+                        const int32_t* row_slot, int epilogue, void* out, int64_t out_sm,
+                        int64_t out_rows, void* stream);
+
+/* out bf16 [tokens, hidden] (row stride out_sm) = bf16(sum over k of
+ * y[t * top_k + k, :]) with y bf16 [tokens * top_k, hidden] contiguous; the
+ * fp32 sum runs in k order (deterministic). */
+int qg_moe_combine(const void* y, int64_t tokens, int top_k, int64_t hidden, void* out, int64_t out_sm,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

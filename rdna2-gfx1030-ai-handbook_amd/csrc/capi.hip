@@ -481,3 +481,119 @@ extern "C" int qg_fp8w_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_
   p.out_dtype = out_dtype;
   return qg::launch_wd_fp8(p, s);  // k == 0: no stage, out = bias (or 0)
 }
+
+// ------------------------------------------------------------------- MoE
+namespace {
+
+bool moe_sizes(int64_t tokens, int n_experts, int top_k, int pad, int64_t* rows_max, int64_t* tiles_max) {
+  if (tokens < 0 || n_experts < 1 || n_experts > 64 || top_k < 1 || top_k > n_experts || pad < 1 || pad > 4096)
+    return false;
+  const int64_t rows = tokens * top_k + static_cast<int64_t>(n_experts) * (pad - 1);
+  if (rows >= (int64_t(1) << 30)) return false;
+  *rows_max = rows;
+  *tiles_max = (rows + QG_MOE_TILE_ROWS - 1) / QG_MOE_TILE_ROWS + n_experts;
+  return true;
+}
+
+}  // namespace
+
+extern "C" int qg_moe_sizes(int64_t tokens, int n_experts, int top_k, int pad, int64_t* rows_max,
+                            int64_t* tiles_max) {
+  if (!rows_max || !tiles_max) return hipErrorInvalidValue;
+  return moe_sizes(tokens, n_experts, top_k, pad, rows_max, tiles_max) ? hipSuccess : hipErrorInvalidValue;
+}
+
+extern "C" int qg_moe_dispatch(const float* logits, int64_t l_sm, int64_t tokens, int n_experts, int top_k,
+                               int pad, int32_t* experts, float* weights, int32_t* counts, int32_t* row_token,
+                               float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,
+                               int64_t tiles_max, void* stream) {
+  int64_t need_rows = 0, need_tiles = 0;
+  if (!moe_sizes(tokens, n_experts, top_k, pad, &need_rows, &need_tiles)) return hipErrorInvalidValue;
+  if (rows_max < need_rows || tiles_max < need_tiles || rows_max >= (int64_t(1) << 30) ||
+      tiles_max >= (int64_t(1) << 30))
+    return hipErrorInvalidValue;
+  if (l_sm < n_experts || (tokens > 0 && (!logits || !experts || !weights))) return hipErrorInvalidValue;
+  if (!counts || !row_token || !row_weight || !row_slot || !tiles) return hipErrorInvalidValue;
+  if (tokens * l_sm >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  qg::MoeDispatchArgs p{};
+  p.logits = logits;
+  p.l_sm = l_sm;
+  p.T = static_cast<int>(tokens);
+  p.E = n_experts;
+  p.top_k = top_k;
+  p.pad = pad;
+  p.experts = experts;
+  p.weights = weights;
+  p.counts = counts;
+  p.row_token = row_token;
+  p.row_weight = row_weight;
+  p.row_slot = row_slot;
+  p.rows_max = static_cast<int>(rows_max);
+  p.tiles = tiles;
+  p.tiles_max = static_cast<int>(tiles_max);
+  p.tile_rows = QG_MOE_TILE_ROWS;
+  return qg::launch_moe_dispatch(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qg_moe_grouped_gemm(const int8_t* a, int64_t a_sm, int64_t a_rows, const int32_t* row_token,
+                                   int64_t rows_max, int64_t k, const int8_t* w, int64_t w_sn, int64_t w_estride,
+                                   int64_t n, int n_experts, const int32_t* tiles, int64_t tiles_max,
+                                   const float* a_scale, const float* b_scale, const float* row_weight,
+                                   const int32_t* row_slot, int epilogue, void* out, int64_t out_sm,
+                                   int64_t out_rows, void* stream) {
+  if (epilogue < QG_MOE_EPI_I32 || epilogue > QG_MOE_EPI_ROUTE) return hipErrorInvalidValue;
+  if (a_rows < 1 || rows_max < 1 || k < 1 || n < 1 || n_experts < 1 || tiles_max < 0) return hipErrorInvalidValue;
+  if (k % kStageK != 0 || a_sm < k || a_sm % 16 != 0 || w_sn < k || w_sn % 16 != 0 || w_estride < n * w_sn ||
+      w_estride % 16 != 0)
+    return hipErrorInvalidValue;
+  if (!a || !w || !tiles || !out || !aligned16(a) || !aligned16(w)) return hipErrorInvalidValue;
+  // 32-bit byte offsets from the A base and from each expert's W base
+  if (a_rows * a_sm >= kMaxOperandBytes || n * w_sn >= kMaxOperandBytes || rows_max >= (int64_t(1) << 30) ||
+      tiles_max >= (int64_t(1) << 24))
+    return hipErrorInvalidValue;
+  if (!row_token && a_rows < rows_max) return hipErrorInvalidValue;
+  const int64_t out_cols = epilogue == QG_MOE_EPI_SILU_MUL ? n / 2 : n;
+  if (out_sm < out_cols) return hipErrorInvalidValue;
+  // rows of out: every routed row (int32 / SiLU*mul) or every slot (route)
+  if (out_rows < 1 || out_rows >= (int64_t(1) << 30) || out_rows * out_sm >= (int64_t(1) << 31) ||
+      (epilogue != QG_MOE_EPI_ROUTE && out_rows < rows_max))
+    return hipErrorInvalidValue;
+  if (epilogue != QG_MOE_EPI_I32 && (!a_scale || !b_scale)) return hipErrorInvalidValue;
+  if (epilogue == QG_MOE_EPI_SILU_MUL && n % 32 != 0) return hipErrorInvalidValue;
+  if (epilogue == QG_MOE_EPI_ROUTE && (!row_weight || !row_slot)) return hipErrorInvalidValue;
+  if (tiles_max == 0) return hipSuccess;
+  qg::I8GemmArgs p{};
+  p.a = a;
+  p.a_sm = a_sm;
+  p.w = w;
+  p.w_sn = w_sn;
+  p.M = static_cast<int>(rows_max);
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(k);
+  p.a_scale = a_scale;
+  p.b_scale = b_scale;
+  p.out = out;
+  p.tiles = tiles;
+  p.tiles_max = static_cast<int>(tiles_max);
+  p.row_token = row_token;
+  p.a_rows = static_cast<int>(a_rows);
+  p.w_estride = w_estride;
+  p.row_weight = row_weight;
+  p.row_slot = row_slot;
+  p.out_sm = out_sm;
+  p.out_rows = static_cast<int>(out_rows);
+  p.n_experts = n_experts;
+  p.moe_epi = epilogue;
+  return qg::launch_i8_moe_gemm(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qg_moe_combine(const void* y, int64_t tokens, int top_k, int64_t hidden, void* out, int64_t out_sm,
+                              void* stream) {
+  if (tokens < 0 || top_k < 1 || hidden < 1 || out_sm < hidden) return hipErrorInvalidValue;
+  if (tokens == 0) return hipSuccess;
+  if (!y || !out || tokens * top_k * hidden >= (int64_t(1) << 31) || tokens * out_sm >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  return qg::launch_moe_combine(static_cast<const uint16_t*>(y), static_cast<int>(tokens), top_k,
+                                static_cast<int>(hidden), static_cast<uint16_t*>(out), out_sm,
+                                static_cast<hipStream_t>(stream));
+}

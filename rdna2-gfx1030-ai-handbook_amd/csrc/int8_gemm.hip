@@ -50,9 +50,9 @@ enum EpiMode { EPI_INT = 0, EPI_F = 1, EPI_FMA = 2, EPI_EAGER = 3, EPI_GELU = 4 
 
 // Tile geometry: BM x BN output tile, WGM x WGN waves, A ring of NA slots and
 // W ring of 2 slots of 128-byte K stages, epilogue parameters after the rings.
-template <int BM_, int BN_, int WGM, int WGN, int NA_>
+template <int BM_, int BN_, int WGM_, int WGN_, int NA_>
 struct I8Geo {
-  static constexpr int BM = BM_, BN = BN_, NA = NA_;
+  static constexpr int BM = BM_, BN = BN_, NA = NA_, WGM = WGM_, WGN = WGN_;
   static constexpr int NW = WGM * WGN, THREADS = 64 * NW;
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave sub-tile
   static constexpr int FM = WM / 32, FN = WN / 32;    // 32x32 blocks per wave
@@ -569,39 +569,25 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_jit(I8GemmArgs p) {
 //          Y: MFMAs of stage s
 constexpr bool kI8PingPong = true;
 
-template <typename G, int OUT, int MODE>
-__global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
-#pragma clang fp contract(off)
+// Copy row offsets per wave of the ping-pong kernels (W copies of waves 0-3,
+// A copies of waves 4-7).
+template <typename G>
+constexpr int pp_copies() { return (G::BM > G::BN ? G::BM : G::BN) / 32; }
+
+// The ping-pong main loop: acc += A tile x W tile^T over S stages of 128 K
+// bytes. voff[i] is this wave's 32-bit byte offset of the row that its copy i
+// fetches (W rows n0 + 8 (gw + 4 i) + (l >> 3) for waves 0-3, A rows for
+// waves 4-7), including the swizzled chunk; a_base / w_base point at K = 0.
+template <typename G>
+__device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* smem, const char* a_base,
+                                            const char* w_base, const uint32_t (&voff)[pp_copies<G>()], int S,
+                                            int wave, int lane) {
   static_assert(G::NW == 8 && G::NA == 3 && G::KT == 4, "ping-pong geometry");
   constexpr int XS = G::BN / 32, YS = G::BM / 32;  // copies per wave and stage (W by X, A by Y)
-  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave >> 1, wc = wave & 1;
+  const int wr = wave / G::WGN, wc = wave % G::WGN;
   const bool grp_x = wave < 4;
   const int gw = wave & 3;
-  int m0, n0;
-  tile_origin<G::BM, G::BN>(p, m0, n0);
-  const EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
-
-  // Copy i of a wave covers rows 8 (gw + 4 i) .. + 7 of its operand's tile;
-  // the 32-bit row offsets (clamped rows, swizzled chunk) are computed once.
-  const CopyPlan<4> plan(grp_x ? n0 : m0, gw, lane);
   const uint32_t smem_base = lds_addr_of(smem);
-  const int S = p.K / G::KS;
-  const char* a_base = reinterpret_cast<const char*>(p.a);
-  const char* w_base = reinterpret_cast<const char*>(p.w);
-  uint32_t voff[YS];
-  {
-    const int rows = grp_x ? p.N : p.M;
-    const uint32_t stride = static_cast<uint32_t>(grp_x ? p.w_sn : p.a_sm);
-    static_for<0, YS>([&](auto i_c) {
-      constexpr int I = decltype(i_c)::value;
-      voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, rows - 1)) * stride + plan.chunk16;
-    });
-  }
   auto copy_w = [&](auto i_c, int s) {
     constexpr int I = decltype(i_c)::value;
     dma16s(w_base + static_cast<int64_t>(s) * G::KS, voff[I],
@@ -618,11 +604,6 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
     a_off[t] = wr * G::WM * G::KS + frag_offset(t, lane);
     b_off[t] = G::RING_B + wc * G::WN * G::KS + frag_offset(t, lane);
   }
-
-  i32x16 acc[G::FM][G::FN];
-  static_for<0, G::FM>([&](auto i) {
-    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
-  });
   i32x4 fa[G::KT][G::FM], fb[G::KT][G::FN];
 
   // Read stage s into the fragment registers with this wave's copies of stage
@@ -688,9 +669,218 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
       }
     }
   }
-
   wait_vm_barrier<0>();  // no copy into LDS in flight; every wave is done reading the rings
+}
+
+template <typename G, int OUT, int MODE>
+__global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
+#pragma clang fp contract(off)
+  constexpr int YS = pp_copies<G>();
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave / G::WGN, wc = wave % G::WGN;
+  const bool grp_x = wave < 4;
+  int m0, n0;
+  tile_origin<G::BM, G::BN>(p, m0, n0);
+  const EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
+
+  // Copy i of a wave covers rows 8 (gw + 4 i) .. + 7 of its operand's tile;
+  // the 32-bit row offsets (clamped rows, swizzled chunk) are computed once.
+  const CopyPlan<4> plan(grp_x ? n0 : m0, wave & 3, lane);
+  uint32_t voff[YS];
+  {
+    const int rows = grp_x ? p.N : p.M;
+    const uint32_t stride = static_cast<uint32_t>(grp_x ? p.w_sn : p.a_sm);
+    static_for<0, YS>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, rows - 1)) * stride + plan.chunk16;
+    });
+  }
+  i32x16 acc[G::FM][G::FN];
+  static_for<0, G::FM>([&](auto i) {
+    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
+  });
+  pp_mainloop<G>(acc, smem, reinterpret_cast<const char*>(p.a), reinterpret_cast<const char*>(p.w), voff,
+                 p.K / G::KS, wave, lane);
   i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
+}
+
+__device__ __forceinline__ float silu(float g) {
+#pragma clang fp contract(off)
+  // g / (1 + e^-g) with the hardware exp2 and reciprocal (a few ulps)
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
+
+// Grouped (MoE) INT8 GEMM on the ping-pong main loop. The grid walks the
+// device tile table (tiles_max 256-row tiles x ceil(N / 192) column tiles):
+// tile t = {expert e (< 0: none), first routed row m0, end of the expert's
+// valid rows}; tile 0's spare field holds the number of tiles in use. A row of routed row r is row_token[r] (or r), W and b_scale
+// start at expert e. Epilogues (v = f32(acc) * (sa[r] * sb[e, n]), order F):
+//   QG_MOE_EPI_I32       out int32 [M, N] = acc (routed rows)
+//   QG_MOE_EPI_SILU_MUL  columns 32 b .. 32 b + 15 are the gate and
+//                        32 b + 16 .. 32 b + 31 the up rows of features
+//                        16 b .. 16 b + 15: out bf16 [M, N / 2] = silu(g) * u
+//   QG_MOE_EPI_ROUTE     out bf16 [slots, N] row row_slot[r] = v * row_weight[r]
+template <typename G, int MOE>
+__global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
+#pragma clang fp contract(off)
+  constexpr int YS = pp_copies<G>();
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES + 8 * G::BM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave / G::WGN, wc = wave % G::WGN;
+  const bool grp_x = wave < 4;
+
+  // Tiles in use (from the dispatch) x column tiles, spread as contiguous
+  // ranges over the 8 XCDs; the rest of the grid exits at once.
+  const int ncol = ceil_div(p.N, G::BN);
+  const int used = min(max(p.tiles[3], 0), p.tiles_max) * ncol;
+  const int bid0 = blockIdx.x;
+  if (bid0 >= ((used + 7) & ~7)) return;
+  const int per_xcd = (used + 7) >> 3;
+  const int bid = (bid0 & 7) * per_xcd + (bid0 >> 3);
+  if (bid >= used) return;
+  const int tile = bid / ncol, ct = bid - tile * ncol;
+  const int e = p.tiles[4 * tile];
+  const int m0 = p.tiles[4 * tile + 1], m_end = p.tiles[4 * tile + 2];
+  // whole workgroup: no tile, or a table entry outside the operands
+  if (e < 0 || e >= p.n_experts || m0 < 0 || m0 >= p.M || m_end <= m0 || m_end > p.M) return;
+  const int n0 = ct * G::BN;
+
+  // per-row / per-column parameters (rows clamped into the routed-row arrays)
+  float ld_sa = 0.0f, ld_sb = 0.0f, ld_rw = 0.0f;
+  int ld_dst = -1;
+  if (tid < G::BM) {
+    const int r = min(m0 + tid, p.M - 1);
+    const int src = p.row_token ? min(max(p.row_token[r], 0), p.a_rows - 1) : min(r, p.a_rows - 1);
+    if constexpr (MOE != QG_MOE_EPI_I32) ld_sa = p.a_scale[src];
+    if constexpr (MOE == QG_MOE_EPI_ROUTE) {
+      ld_rw = p.row_weight[r];
+      ld_dst = p.row_slot[r];
+    }
+  }
+  if constexpr (MOE != QG_MOE_EPI_I32) {
+    if (tid < G::BN) ld_sb = p.b_scale[static_cast<int64_t>(e) * p.N + min(n0 + tid, p.N - 1)];
+  }
+
+  const CopyPlan<4> plan(grp_x ? n0 : m0, wave & 3, lane);
+  uint32_t voff[YS];
+  static_for<0, YS>([&](auto i_c) {
+    constexpr int I = decltype(i_c)::value;
+    if (grp_x) {
+      voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, p.N - 1)) * static_cast<uint32_t>(p.w_sn) +
+                plan.chunk16;
+    } else {
+      const int r = min(plan.row0 + 32 * I, p.M - 1);
+      const int src = p.row_token ? min(max(p.row_token[r], 0), p.a_rows - 1) : min(r, p.a_rows - 1);
+      voff[I] = static_cast<uint32_t>(src) * static_cast<uint32_t>(p.a_sm) + plan.chunk16;
+    }
+  });
+  i32x16 acc[G::FM][G::FN];
+  static_for<0, G::FM>([&](auto i) {
+    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
+  });
+  pp_mainloop<G>(acc, smem, reinterpret_cast<const char*>(p.a),
+                 reinterpret_cast<const char*>(p.w) + static_cast<int64_t>(e) * p.w_estride, voff, p.K / G::KS,
+                 wave, lane);
+
+  // ---- epilogue: parameters through LDS (the rings are free now) ------------
+  // row weights / output rows sit after the GEMM's own parameter area
+  float* sa_lds = reinterpret_cast<float*>(smem + G::SC_A);
+  float* sb_lds = reinterpret_cast<float*>(smem + G::SC_B);
+  float* rw_lds = reinterpret_cast<float*>(smem + G::LDS_BYTES);
+  int* dst_lds = reinterpret_cast<int*>(smem + G::LDS_BYTES + G::BM * 4);
+  if (tid < G::BM) {
+    sa_lds[tid] = ld_sa;
+    rw_lds[tid] = ld_rw;
+    dst_lds[tid] = ld_dst;
+  }
+  if (tid < G::BN) sb_lds[tid] = ld_sb;
+  __syncthreads();
+  const int lh = 4 * (lane >> 5);
+  const int lcol = lane & 31;
+  // bf16 outputs whose rows take whole 16-byte chunks are staged per wave in
+  // LDS and written as row chunks; int32 (test) output goes element-wise
+  constexpr bool STAGED = MOE != QG_MOE_EPI_I32;
+  constexpr int OCOLS = MOE == QG_MOE_EPI_SILU_MUL ? G::WN / 2 : G::WN;  // output columns per wave row
+  constexpr int ROWB = OCOLS * 2 + 16;
+  constexpr int CH = OCOLS * 2 / 16;
+  static_assert(G::WM * ROWB <= G::RING / G::NW, "staging region");
+  const int out_cols = MOE == QG_MOE_EPI_SILU_MUL ? p.N / 2 : p.N;
+  const bool staged = STAGED && (out_cols % 8) == 0 && (p.out_sm % 8) == 0 &&
+                      (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+  char* region = smem + wave * (G::RING / G::NW);
+  float sbv[G::FN];
+  static_for<0, G::FN>([&](auto j) { sbv[j] = sb_lds[wc * G::WN + j * 32 + lcol]; });
+  static_for<0, G::FM>([&](auto i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // rows 32 i + 8 q + lh + (0..3) of the wave sub-tile: aligned LDS vectors
+      const int rw0 = 32 * i + 8 * q + lh;
+      const f32x4 sa4 = *reinterpret_cast<const f32x4*>(sa_lds + wr * G::WM + rw0);
+      f32x4 rw4 = {0, 0, 0, 0};
+      if constexpr (MOE == QG_MOE_EPI_ROUTE) rw4 = *reinterpret_cast<const f32x4*>(rw_lds + wr * G::WM + rw0);
+      static_for<0, G::FN>([&](auto j) {
+        const int cl = wc * G::WN + j * 32 + lcol;  // tile column of this lane
+        const int n = n0 + cl;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int rw_ = rw0 + r4;          // row in the wave sub-tile
+          const int rl = wr * G::WM + rw_;   // tile row
+          const int row = m0 + rl;
+          const int32_t a = acc[i][j][4 * q + r4];
+          if constexpr (MOE == QG_MOE_EPI_I32) {
+            if (row < m_end && n < p.N) static_cast<int32_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + n] = a;
+          } else {
+            const float v = static_cast<float>(a) * (sa4[r4] * sbv[j]);
+            if constexpr (MOE == QG_MOE_EPI_SILU_MUL) {
+              const float u = __shfl_xor(v, 16, 64);  // up value of this gate lane's feature
+              if ((lane & 16) == 0) {
+                const uint16_t bits = f32_to_bf16(silu(v) * u);
+                if (staged) {
+                  *reinterpret_cast<uint16_t*>(region + rw_ * ROWB + (16 * j + (lane & 15)) * 2) = bits;
+                } else if (row < m_end && n < p.N) {
+                  const int feat = ((n0 + wc * G::WN + j * 32) >> 5) * 16 + (lane & 15);
+                  static_cast<uint16_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + feat] = bits;
+                }
+              }
+            } else {
+              const uint16_t bits = f32_to_bf16(v * rw4[r4]);
+              if (staged) {
+                *reinterpret_cast<uint16_t*>(region + rw_ * ROWB + (j * 32 + lcol) * 2) = bits;
+              } else {
+                const int d = dst_lds[rl];
+                if (row < m_end && d >= 0 && d < p.out_rows && n < p.N)
+                  static_cast<uint16_t*>(p.out)[static_cast<int64_t>(d) * p.out_sm + n] = bits;
+              }
+            }
+          }
+        }
+      });
+    }
+  });
+  if constexpr (STAGED) {
+    if (staged) {
+      // LDS accesses of one wave complete in order: the reads see the writes
+      const int col0 = (MOE == QG_MOE_EPI_SILU_MUL ? (n0 + wc * G::WN) / 2 : n0 + wc * G::WN);
+      for (int c = lane; c < G::WM * CH; c += 64) {
+        const int rr = c / CH, cc = c - rr * CH;
+        const int rl = wr * G::WM + rr;
+        const int row = m0 + rl;
+        const int d = MOE == QG_MOE_EPI_ROUTE ? dst_lds[rl] : row;
+        const int col = col0 + cc * 8;
+        if (row < m_end && d >= 0 && d < p.out_rows && col + 8 <= out_cols) {
+          const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
+          *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(p.out) + static_cast<int64_t>(d) * p.out_sm + col) = v;
+        }
+      }
+    }
+  }
 }
 
 template <typename G, int WPE, int OUT, int MODE>
@@ -726,6 +916,25 @@ hipError_t launch_variant(const I8GemmArgs& p, hipStream_t stream) {
 }
 
 }  // namespace
+
+hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream) {
+  // 192-row tiles: expert segments of ~512-576 rows (cfg4) fill 3 tiles
+  using G = I8Geo<QG_MOE_TILE_ROWS, 256, 2, 4, 3>;
+  static_assert(G::LDS_BYTES <= 160 * 1024, "LDS per CU");
+  const int blocks = p.tiles_max * ceil_div(p.N, G::BN);
+  if (blocks == 0) return hipSuccess;
+  switch (p.moe_epi) {
+    case QG_MOE_EPI_I32:
+      hipLaunchKernelGGL((k_i8_moe_pp<G, QG_MOE_EPI_I32>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
+      break;
+    case QG_MOE_EPI_SILU_MUL:
+      hipLaunchKernelGGL((k_i8_moe_pp<G, QG_MOE_EPI_SILU_MUL>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
+      break;
+    default:
+      hipLaunchKernelGGL((k_i8_moe_pp<G, QG_MOE_EPI_ROUTE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0) return hipSuccess;

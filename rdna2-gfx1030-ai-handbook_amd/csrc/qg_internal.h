@@ -22,9 +22,46 @@ struct I8GemmArgs {
   void* out;             // [M, N] contiguous
   int out_dtype;
   int epi;
+  // Grouped (MoE) mode (launch_i8_moe_gemm): M is the number of routed rows,
+  // tiles [tiles_max][4] = {expert (< 0: none), first row, end of valid rows, -};
+  // A row of routed row r is row_token[r] (r when null, < a_rows); expert e's
+  // weights start w_estride bytes after expert e-1's, its scales N floats.
+  const int* tiles;
+  int tiles_max;
+  const int* row_token;
+  int a_rows;
+  int64_t w_estride;
+  const float* row_weight;
+  const int* row_slot;
+  int64_t out_sm;
+  int out_rows;   // rows of out (routed rows, or tokens * top_k for the route epilogue)
+  int n_experts;
+  int moe_epi;
 };
 
 hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream);
+hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream);
+
+// MoE routing and dispatch: see include/qgemm.h (qg_moe_dispatch).
+struct MoeDispatchArgs {
+  const float* logits;
+  int64_t l_sm;
+  int T, E, top_k, pad;
+  int* experts;       // [T, top_k]
+  float* weights;     // [T, top_k]
+  int* counts;        // [3 E]: counts, offsets, cursors
+  int* row_token;     // [rows_max]
+  float* row_weight;  // [rows_max]
+  int* row_slot;      // [rows_max]
+  int rows_max;
+  int* tiles;         // [tiles_max][4]
+  int tiles_max;
+  int tile_rows;
+};
+hipError_t launch_moe_dispatch(const MoeDispatchArgs& p, hipStream_t stream);
+// out[t, n] = bf16(sum over k of y[t * top_k + k, n]) (fp32 sum in k order)
+hipError_t launch_moe_combine(const uint16_t* y, int T, int top_k, int H, uint16_t* out, int64_t out_sm,
+                              hipStream_t stream);
 
 // dst[r, k] = src[r * s_r + k * s_k] for k < K, 0 for K <= k < k_pad.
 hipError_t launch_pack_rows_i8(const int8_t* src, int64_t s_r, int64_t s_k,

@@ -338,7 +338,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_skinny(W4Args p) {
 // ------------------------------------------------------------- decode kernel
 // M <= 16 (token decode), the HBM-bound shape. One workgroup of WAVES waves
 // per 16*CT output columns; wave w owns a contiguous range of 128-wide K
-// chunks (at most kDecodeChunks). At the start each wave copies its
+// chunks (at most CH, 4 or 8). At the start each wave copies its
 // activation slice [rows, 128 * chunks] into its own LDS region (one 16-byte
 // load and one 16-byte LDS store per lane per row and 512 K), storing every
 // 8-element group in the order (0 2 4 6 1 3 5 7). In that order a weight
@@ -350,10 +350,10 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_skinny(W4Args p) {
 // The activation fragments (ds_read_b128) and the MFMA against ones that
 // yields the row sums per group are shared by the CT column tiles. All
 // weight, scale and zero-point loads of a wave are issued before its first
-// MFMA (the chunk range is at most kDecodeChunks long), unconditionally and
+// MFMA (the chunk range is at most CH long), unconditionally and
 // clamped as in the skinny kernel; the WAVES partial tiles are summed through
 // LDS in a fixed order.
-constexpr int kDecodeChunks = 4;
+constexpr int kDecodeChunks = 4;  // chunks per wave with 8 waves (K <= 4096)
 
 template <bool F16A, bool UINT4>
 struct Unpack7 {
@@ -414,12 +414,13 @@ struct DecodeChunk {
 };
 
 // RP: activation rows held per slab (1, 4 or 16; rows past M repeat row M-1).
-template <int RP, int CT, int G, bool KN, bool F16A, int WAVES, bool UINT4>
+// CH: 128-wide K chunks per wave (4 or 8).
+template <int RP, int CT, int G, bool KN, bool F16A, int WAVES, bool UINT4, int CH>
 __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
 #pragma clang fp contract(off)
   constexpr int SPC = 128 / G;                  // groups per chunk
   constexpr int STEPS_PER_GROUP = 4 / SPC;
-  constexpr int CH = kDecodeChunks;
+  static_assert(CH == 4 || CH == 8, "chunks per wave");
   constexpr int ROWB = CH * 128 * 2 + 16;       // LDS bytes per activation row (padded)
   constexpr float MAGIC = F16A ? 256.0f : 128.0f;
   constexpr float UNIT = F16A ? 4.0f : 1.0f;
@@ -460,16 +461,18 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
   }
 
   // ---- 2. every weight / scale / zero load of this wave, in chunk order ----
-  // UINT4 (group 128: chunk c is group c; launcher: 4 chunks per wave and
-  // ng % 4 == 0): the wave's 4 groups start at a multiple of 4, so one 8-byte
-  // load holds their bf16 scales and one word their zero points (nibbles
-  // 4 * (g0 % 8) + 4 cl). Waves past K read an aligned in-range quad.
-  uint2 s4[CT];
+  // UINT4 (group 128: chunk c is group c; launcher: CH chunks per wave and
+  // ng % CH == 0): the wave's CH groups start at a multiple of CH, so CH / 4
+  // 8-byte loads hold their bf16 scales and one word their zero points
+  // (nibbles 4 * (g0 % 8) + 4 cl). Waves past K read an aligned in-range set.
+  uint2 s4[CT][CH / 4];
   uint32_t z8[CT];
-  const int g0 = min(c0, (p.ng - 1) & ~3);
+  const int g0 = min(c0, (p.ng - 1) & ~(CH - 1));
   if constexpr (UINT4) {
     static_for<0, CT>([&](auto t) {
-      s4[t] = load_at<uint2>(p.scales, 2u * (static_cast<uint32_t>(ncol[t]) * p.ng + g0));
+      static_for<0, CH / 4>([&](auto h) {
+        s4[t][h] = load_at<uint2>(p.scales, 2u * (static_cast<uint32_t>(ncol[t]) * p.ng + g0 + 4 * h));
+      });
       z8[t] = load_at<uint32_t>(p.zeros, 4u * (static_cast<uint32_t>(ncol[t]) * p.zw + (g0 >> 3)));
     });
   }
@@ -520,7 +523,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
     static_for<0, CT>([&](auto t) {
       const uint32_t zs = z8[t] >> (4 * (g0 & 7));
       static_for<0, CH>([&](auto cl) {
-        const uint32_t sw = (cl >> 1) ? s4[t].y : s4[t].x;
+        const uint32_t sw = ((cl >> 1) & 1) ? s4[t][cl >> 2].y : s4[t][cl >> 2].x;
         gs[t][cl] = __uint_as_float((cl & 1) ? (sw & 0xFFFF0000u) : (sw << 16)) / UNIT;
         if (cl >= nch) gs[t][cl] = 0.0f;
         gz[t][cl] = MAGIC + UNIT * static_cast<float>((zs >> (4 * cl)) & 15u);
@@ -705,14 +708,13 @@ hipError_t launch_skinny_g(const W4Args& p, hipStream_t stream) {
   }
 }
 
-template <int RP, int CT, int G, bool KN, bool F16A, bool UINT4>
+template <int RP, int CT, int G, bool KN, bool F16A, bool UINT4, int WAVES = 8, int CH = kDecodeChunks>
 hipError_t launch_decode_t(const W4Args& p, hipStream_t stream) {
-  constexpr int WAVES = 8;
-  const size_t a_bytes = static_cast<size_t>(WAVES) * RP * (kDecodeChunks * 256 + 16);
+  const size_t a_bytes = static_cast<size_t>(WAVES) * RP * (CH * 256 + 16);
   const size_t red_bytes = static_cast<size_t>(WAVES) * 16 * (16 * CT + 1) * 4;
   const size_t lds = a_bytes > red_bytes ? a_bytes : red_bytes;
   dim3 grid(ceil_div(p.N, 16 * CT), ceil_div(p.M, RP));
-  hipLaunchKernelGGL((k_w4_decode<RP, CT, G, KN, F16A, WAVES, UINT4>), grid, dim3(64 * WAVES), lds, stream, p);
+  hipLaunchKernelGGL((k_w4_decode<RP, CT, G, KN, F16A, WAVES, UINT4, CH>), grid, dim3(64 * WAVES), lds, stream, p);
   return hipGetLastError();
 }
 

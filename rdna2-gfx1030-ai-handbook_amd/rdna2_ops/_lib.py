@@ -38,6 +38,12 @@ W4_SIGNED_NIBBLES = 1
 W4_ORDER_HIGH = 2
 W4_LAYOUT_KN = 4
 W4_ZEROS_PACKED = 8
+# enum qg_moe_epilogue, QG_MOE_TILE_ROWS
+MOE_EPI_I32 = 0
+MOE_EPI_SILU_MUL = 1
+MOE_EPI_ROUTE = 2
+MOE_TILE_ROWS = 192
+MOE_COUNTS_PER_EXPERT = 259
 
 _p, _i, _i64, _sz, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
 
@@ -61,6 +67,11 @@ SIGNATURES = {
     "qg_fp8w_gemm_workspace_bytes": (_sz, [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64]),
     "qg_fp8w_gemm": (_i, [_p, _i, _i64, _i64, _i64, _i64, _p, _i, _i64, _i64, _i64, _p, _p, _i, _p, _i,
                           _p, _sz, _p]),
+    "qg_moe_sizes": (_i, [_i64, _i, _i, _i, _p, _p]),
+    "qg_moe_dispatch": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p]),
+    "qg_moe_grouped_gemm": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i, _p, _i64, _p, _p,
+                                 _p, _p, _i, _p, _i64, _i64, _p]),
+    "qg_moe_combine": (_i, [_p, _i64, _i, _i64, _p, _i64, _p]),
 }
 
 

@@ -52,3 +52,25 @@ def cfg1(m=4096, hidden=3072, seed=1) -> Cfg1:
         b = torch.randn(n, generator=g) * 0.01
         ws += [w.to(torch.float16), b.to(torch.float16)]
     return Cfg1(x.to(torch.float16), *ws)
+
+
+@dataclass
+class Cfg4:
+    x: torch.Tensor        # bf16 [T, H]
+    logits: torch.Tensor   # fp32 [T, E]
+    w_gate: torch.Tensor   # fp32 [E, F, H]
+    w_up: torch.Tensor     # fp32 [E, F, H]
+    w_down: torch.Tensor   # fp32 [E, H, F]
+    top_k: int
+
+
+def cfg4(tokens=4096, hidden=2048, experts=64, inter=768, top_k=8, seed=4) -> Cfg4:
+    """MoE prefill grouped INT8 GEMM: router logits and
+    activations N(0, 1), expert weights N(0, 0.02), drawn in this order."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(tokens, experts, generator=g)
+    x = torch.randn(tokens, hidden, generator=g).to(torch.bfloat16)
+    w_gate = torch.randn(experts, inter, hidden, generator=g) * 0.02
+    w_up = torch.randn(experts, inter, hidden, generator=g) * 0.02
+    w_down = torch.randn(experts, hidden, inter, generator=g) * 0.02
+    return Cfg4(x, logits, w_gate, w_up, w_down, top_k)

@@ -17,15 +17,16 @@
 //    cycles) whatever the depth in flight, about what a 256 x 192 tile needs at
 //    the full MFMA rate, and a wave blocked issuing a copy cannot issue MFMAs.
 //    Two pipelines:
-//      - 8 waves (2 per SIMD, 64 x 96 each) read each 32-byte k-step's
-//        fragments from LDS just in time; one barrier per stage; while one
-//        wave of a SIMD waits on a copy the other keeps the MFMA pipe busy
-//        (large problems);
+//      - 8 waves, two per SIMD, in two groups that alternate every half
+//        stage between a burst of MFMAs and reading / copying the next
+//        stage ("ping-pong", large problems and the grouped MoE GEMM);
+//        their accumulators hold the transposed tile so that each lane owns
+//        runs of 4 adjacent output columns (paired conversions, vector LDS
+//        staging in the epilogue);
 //      - 4 waves (1 per SIMD) stage the whole next stage in registers while
 //        the current one computes, two barriers per stage (small tiles, two
-//        workgroups per CU);
-//    Waits are branch-free: past the end the last stage is re-copied into its
-//    own slot (identical bytes, never a different stage's);
+//        workgroups per CU); past the end it re-copies the last stage into
+//        its own slot (identical bytes) to keep its waits branch-free;
 //  * LDS rows are 128 bytes with the 16-byte chunk index XOR-swizzled by
 //    ((row >> 1) & 7): the DMA writes whole 1 KB blocks and every group of 16
 //    lanes of a fragment read touches 16 distinct 16-byte bank groups;
@@ -45,6 +46,9 @@ namespace qg {
 namespace {
 
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 enum EpiMode { EPI_INT = 0, EPI_F = 1, EPI_FMA = 2, EPI_EAGER = 3, EPI_GELU = 4 };
 
@@ -114,24 +118,29 @@ constexpr int out_size() { return (OUT == QG_F16 || OUT == QG_BF16) ? 2 : 4; }
 //   EPI_EAGER: t = out(f32(acc) * (sa * sb)); t = out(t + out(bias))  (comfy_int8.py:128-143)
 //   EPI_GELU:  EPI_F followed by GELU-tanh in fp32
 template <int OUT, int MODE>
-__device__ __forceinline__ uint32_t epi_bits(int32_t acc, float sa, float sb, float bv, bool has_bias) {
+__device__ __forceinline__ float epi_value(int32_t acc, float sa, float sb, float bv, bool has_bias) {
 #pragma clang fp contract(off)
+  const float scale = sa * sb;
+  const float accf = static_cast<float>(acc);
+  float v;
+  if constexpr (MODE == EPI_EAGER) {
+    v = round_to<OUT>(accf * scale);
+    if (has_bias) v = v + round_to<OUT>(bv);
+  } else if constexpr (MODE == EPI_FMA) {
+    v = has_bias ? __builtin_fmaf(accf, scale, bv) : accf * scale;
+  } else {
+    v = accf * scale;
+    if (has_bias) v = v + bv;
+    if constexpr (MODE == EPI_GELU) v = gelu_tanh(v);
+  }
+  return v;
+}
+template <int OUT, int MODE>
+__device__ __forceinline__ uint32_t epi_bits(int32_t acc, float sa, float sb, float bv, bool has_bias) {
   if constexpr (MODE == EPI_INT) {
     return static_cast<uint32_t>(acc);
   } else {
-    const float scale = sa * sb;
-    const float accf = static_cast<float>(acc);
-    float v;
-    if constexpr (MODE == EPI_EAGER) {
-      v = round_to<OUT>(accf * scale);
-      if (has_bias) v = v + round_to<OUT>(bv);
-    } else if constexpr (MODE == EPI_FMA) {
-      v = has_bias ? __builtin_fmaf(accf, scale, bv) : accf * scale;
-    } else {
-      v = accf * scale;
-      if (has_bias) v = v + bv;
-      if constexpr (MODE == EPI_GELU) v = gelu_tanh(v);
-    }
+    const float v = epi_value<OUT, MODE>(acc, sa, sb, bv, has_bias);
     if constexpr (OUT == QG_F32) return __float_as_uint(v);
     else if constexpr (OUT == QG_F16) return f32_to_f16(v);
     else return f32_to_bf16(v);
@@ -459,101 +468,6 @@ __global__ __launch_bounds__(G::THREADS, WPE) void k_i8_gemm(I8GemmArgs p) {
   i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
 }
 
-// 8 waves (WGM x WGN with WGN = 2, two per SIMD), fragments read from LDS one
-// k-step ahead, one barrier per stage:
-//   barrier    : A and W of stage s landed everywhere (the newest copy group,
-//                A of stage s+1, may still be in flight: vmcnt(A_SEGS)), and
-//                every wave is done with stage s-1's slots
-//   copies     : W of stage s+1 into the W slot of stage s-1, then A of stage
-//                s+2 into the A slot of stage s-1, spread over the k-steps
-//   k-steps    : read k-step t+1's fragments, MFMAs of k-step t
-template <typename G, int OUT, int MODE>
-__global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_jit(I8GemmArgs p) {
-#pragma clang fp contract(off)
-  static_assert(G::NA == 3, "JIT pipeline keeps A two stages ahead");
-  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave >> 1, wc = wave & 1;
-  int m0, n0;
-  tile_origin<G::BM, G::BN>(p, m0, n0);
-  const EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
-
-  const CopyPlan<G::NW> ca(m0, wave, lane), cw(n0, wave, lane);
-  const uint32_t smem_base = lds_addr_of(smem);
-  const int S = p.K / G::KS;
-  const char* a_base = reinterpret_cast<const char*>(p.a);
-  const char* w_base = reinterpret_cast<const char*>(p.w);
-  auto dma_a = [&](auto i_c, int s) {
-    ca.template copy<decltype(i_c)::value>(a_base, p.a_sm, p.M, s, smem_base + (s % 3) * G::STAGE_A, wave);
-  };
-  auto dma_w = [&](auto i_c, int s) {
-    cw.template copy<decltype(i_c)::value>(w_base, p.w_sn, p.N, s, smem_base + G::RING_B + (s & 1) * G::STAGE_B,
-                                           wave);
-  };
-
-  int a_off[G::KT], b_off[G::KT];
-#pragma unroll
-  for (int t = 0; t < G::KT; ++t) {
-    a_off[t] = wr * G::WM * G::KS + frag_offset(t, lane);
-    b_off[t] = G::RING_B + wc * G::WN * G::KS + frag_offset(t, lane);
-  }
-
-  i32x16 acc[G::FM][G::FN];
-  static_for<0, G::FM>([&](auto i) {
-    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
-  });
-  i32x4 fa[2][G::FM], fb[2][G::FN];  // [k-step parity][block]
-
-  auto read_step = [&](auto t_c, auto buf_c, int abase, int bbase) {
-    constexpr int t = decltype(t_c)::value, buf = decltype(buf_c)::value;
-    static_for<0, G::FM>([&](auto i) {
-      fa[buf][i] = *reinterpret_cast<const i32x4*>(smem + abase + a_off[t] + i * 32 * G::KS);
-    });
-    static_for<0, G::FN>([&](auto j) {
-      fb[buf][j] = *reinterpret_cast<const i32x4*>(smem + bbase + b_off[t] + j * 32 * G::KS);
-    });
-  };
-
-  if (S > 0) {
-    // prologue: A(0), W(0), A(1) in flight
-    static_for<0, G::A_SEGS>([&](auto i) { dma_a(i, 0); });
-    static_for<0, G::B_SEGS>([&](auto i) { dma_w(i, 0); });
-    static_for<0, G::A_SEGS>([&](auto i) { dma_a(i, min(1, S - 1)); });
-    constexpr int COPIES = G::A_SEGS + G::B_SEGS;  // per wave and stage, spread over KT k-steps
-    for (int s = 0; s < S; ++s) {
-      wait_vm_barrier<G::A_SEGS>();
-      const int abase = (s % 3) * G::STAGE_A;
-      const int bbase = (s & 1) * G::STAGE_B;
-      const int w_next = min(s + 1, S - 1), a_next = min(s + 2, S - 1);
-      read_step(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, abase, bbase);
-      static_for<0, G::KT>([&](auto t_c) {
-        constexpr int t = decltype(t_c)::value;
-        if constexpr (t + 1 < G::KT)
-          read_step(std::integral_constant<int, t + 1>{}, std::integral_constant<int, (t + 1) & 1>{}, abase, bbase);
-        constexpr int d0 = t * COPIES / G::KT, d1 = (t + 1) * COPIES / G::KT;
-        static_for<d0, d1>([&](auto d) {
-          constexpr int di = decltype(d)::value;
-          if constexpr (di < G::B_SEGS) dma_w(d, w_next);
-          else dma_a(std::integral_constant<int, di - G::B_SEGS>{}, a_next);
-        });
-        __builtin_amdgcn_sched_barrier(0);
-        static_for<0, G::FM>([&](auto i) {
-          static_for<0, G::FN>([&](auto j) {
-            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[t & 1][i], fb[t & 1][j], acc[i][j], 0, 0, 0);
-          });
-        });
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    }
-  }
-
-  wait_vm_barrier<0>();  // no copy into LDS in flight; every wave is done reading the rings
-  i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
-}
-
 // 8 waves in two groups that share the SIMDs pairwise (waves w and w + 4) and
 // alternate roles every half stage ("ping-pong"): while one wave of a SIMD
 // issues its whole stage of MFMAs back to back, the other reads its next
@@ -567,21 +481,35 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_jit(I8GemmArgs p) {
 //          A(s+2) may still fly) and Y's reads of stage s are complete
 //   P2(s)  X: read stage s+1, copy W of stage s+2 into the W slot of stage s
 //          Y: MFMAs of stage s
-constexpr bool kI8PingPong = true;
+// Nothing past the last stage is copied or read: in the last two stages the
+// waits at B1 drain every copy instead.
+//
+// Accumulator layout: W fragments are the MFMA's first operand, so each 32x32
+// block holds the transposed product: register r of lane l is row
+// 32 i + (l & 31) and column 32 j + 8 (r >> 2) + 4 (l >> 5) + (r & 3) of the
+// wave sub-tile. Every register quad is 4 adjacent columns of one row, which
+// the epilogue converts with paired conversions and stores as one vector.
 
 // Copy row offsets per wave of the ping-pong kernels (W copies of waves 0-3,
 // A copies of waves 4-7).
 template <typename G>
 constexpr int pp_copies() { return (G::BM > G::BN ? G::BM : G::BN) / 32; }
 
-// The ping-pong main loop: acc += A tile x W tile^T over S stages of 128 K
-// bytes. voff[i] is this wave's 32-bit byte offset of the row that its copy i
-// fetches (W rows n0 + 8 (gw + 4 i) + (l >> 3) for waves 0-3, A rows for
-// waves 4-7), including the swizzled chunk; a_base / w_base point at K = 0.
-template <typename G>
+// The ping-pong main loop: acc += (A tile x W tile^T) over S stages of 128 K
+// bytes, in the transposed layout above. voff[i] is this wave's 32-bit byte
+// offset of the row that its copy i fetches (W rows n0 + 8 (gw + 4 i) +
+// (l >> 3) for waves 0-3, A rows for waves 4-7), including the swizzled
+// chunk; a_base / w_base point at K = 0. park() runs in every wave once its
+// first copies, and every load it issued before the loop, have landed, and
+// before the barrier that opens the loop: it parks the epilogue parameters in
+// LDS. On return no copy is in flight and every wave has passed the barrier
+// after the last read of the rings, so each wave may stage its epilogue in its
+// own part of the rings at once (group X's epilogue overlaps group Y's last
+// MFMAs).
+template <typename G, typename Park>
 __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* smem, const char* a_base,
                                             const char* w_base, const uint32_t (&voff)[pp_copies<G>()], int S,
-                                            int wave, int lane) {
+                                            int wave, int lane, Park&& park) {
   static_assert(G::NW == 8 && G::NA == 3 && G::KT == 4, "ping-pong geometry");
   constexpr int XS = G::BN / 32, YS = G::BM / 32;  // copies per wave and stage (W by X, A by Y)
   const int wr = wave / G::WGN, wc = wave % G::WGN;
@@ -606,10 +534,11 @@ __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* s
   }
   i32x4 fa[G::KT][G::FM], fb[G::KT][G::FN];
 
-  // Read stage s into the fragment registers with this wave's copies of stage
-  // cs spread between the k-steps (W copies for X, A copies for Y).
-  auto load_phase = [&](auto x_c, int s, int cs) {
+  // Read stage s into the fragment registers; with COPY, this wave's copies of
+  // stage cs are spread between the k-steps (W copies for X, A copies for Y).
+  auto load_phase = [&](auto x_c, auto copy_c, int s, int cs) {
     constexpr bool X = decltype(x_c)::value;
+    constexpr bool COPY = decltype(copy_c)::value;
     const int abase = (s % 3) * G::STAGE_A;
     const int bbase = (s & 1) * G::STAGE_B;
     static_for<0, G::KT>([&](auto t_c) {
@@ -620,9 +549,9 @@ __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* s
       static_for<0, G::FN>([&](auto j) {
         fb[t][j] = *reinterpret_cast<const i32x4*>(smem + bbase + b_off[t] + j * 32 * G::KS);
       });
-      if constexpr (X) {
+      if constexpr (COPY && X) {
         static_for<t * XS / G::KT, (t + 1) * XS / G::KT>([&](auto d) { copy_w(d, cs); });
-      } else {
+      } else if constexpr (COPY) {
         static_for<t * YS / G::KT, (t + 1) * YS / G::KT>([&](auto d) { copy_a(d, cs); });
       }
     });
@@ -632,44 +561,181 @@ __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* s
     static_for<0, G::KT>([&](auto t) {
       static_for<0, G::FM>([&](auto i) {
         static_for<0, G::FN>([&](auto j) {
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[t][i], fb[t][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[t][j], fa[t][i], acc[i][j], 0, 0, 0);
         });
       });
     });
     __builtin_amdgcn_s_setprio(0);
   };
-  using XT_ = std::true_type;
-  using YT_ = std::false_type;
+  using T_ = std::true_type;
+  using F_ = std::false_type;
 
-  // Both groups pass the same barriers: one before the prologue, then B0 and
+  if (S <= 0) {
+    park();
+    wait_lds_barrier();
+    return;
+  }
+  // Both groups pass the same barriers: one after the prologue, then B0 and
   // B1 of every stage.
-  if (S > 0) {
-    if (grp_x) {
-      // prologue: W(0) landed everywhere, then read stage 0 and copy W(1)
-      static_for<0, XS>([&](auto d) { copy_w(d, 0); });
-      wait_vm<0>();
-      __builtin_amdgcn_s_barrier();
-      load_phase(XT_{}, 0, min(1, S - 1));
-      for (int s = 0; s < S; ++s) {
-        __builtin_amdgcn_s_barrier();  // B0(s)
-        mfma_phase();
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1(s)
-        load_phase(XT_{}, min(s + 1, S - 1), min(s + 2, S - 1));
-      }
-    } else {
-      static_for<0, YS>([&](auto d) { copy_a(d, 0); });
-      static_for<0, YS>([&](auto d) { copy_a(d, min(1, S - 1)); });
+  if (grp_x) {
+    // prologue: W(0) landed everywhere, then read stage 0 and copy W(1)
+    static_for<0, XS>([&](auto d) { copy_w(d, 0); });
+    wait_vm<0>();
+    park();
+    wait_lds_barrier();
+    if (S > 1) load_phase(T_{}, T_{}, 0, 1);
+    else load_phase(T_{}, F_{}, 0, 0);
+    for (int s = 0; s < S; ++s) {
+      __builtin_amdgcn_s_barrier();  // B0(s)
+      mfma_phase();
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1(s)
+      if (s + 2 < S) load_phase(T_{}, T_{}, s + 1, s + 2);
+      else if (s + 1 < S) load_phase(T_{}, F_{}, s + 1, 0);
+    }
+  } else {
+    static_for<0, YS>([&](auto d) { copy_a(d, 0); });
+    if (S > 1) {
+      static_for<0, YS>([&](auto d) { copy_a(d, 1); });
       wait_vm<YS>();
-      __builtin_amdgcn_s_barrier();
-      for (int s = 0; s < S; ++s) {
-        __builtin_amdgcn_s_barrier();  // B0(s)
-        load_phase(YT_{}, s, min(s + 2, S - 1));
+    } else {
+      wait_vm<0>();
+    }
+    park();
+    wait_lds_barrier();
+    for (int s = 0; s < S; ++s) {
+      __builtin_amdgcn_s_barrier();  // B0(s)
+      if (s + 2 < S) {
+        load_phase(F_{}, T_{}, s, s + 2);
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(YS) : "memory");  // B1(s)
-        mfma_phase();
+      } else {
+        load_phase(F_{}, F_{}, s, 0);
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1(s)
       }
+      mfma_phase();
     }
   }
-  wait_vm_barrier<0>();  // no copy into LDS in flight; every wave is done reading the rings
+}
+
+// Two fp32 values rounded to nearest-even fp16 / bf16 and packed (first in the
+// low half) by one paired hardware conversion; bit-identical to f32_to_f16 /
+// f32_to_bf16 for every fp32 input, NaNs included.
+template <int OUT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const f32x2 v = {a, b};
+  if constexpr (OUT == QG_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// 4 adjacent floats 32 j + 8 g + lq .. + 3 of a per-column LDS vector.
+__device__ __forceinline__ f32x4 col4(const float* v, int c0) { return *reinterpret_cast<const f32x4*>(v + c0); }
+
+// Epilogue of the dense ping-pong kernel (transposed accumulators; row scales,
+// column scales and fp32 bias values parked at SC_A, SC_B and SC_BIAS).
+// Full tiles are staged per wave in its own part of the rings and leave as
+// whole 16-byte row chunks; edge tiles store element-wise.
+template <typename G, int OUT, int MODE>
+__device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const i32x16 (&acc)[G::FM][G::FN], char* smem,
+                                            int m0, int n0, int wr, int wc, int wave, int lane) {
+#pragma clang fp contract(off)
+  const float* sa_lds = reinterpret_cast<const float*>(smem + G::SC_A);
+  const float* sb_lds = reinterpret_cast<const float*>(smem + G::SC_B);
+  const float* bv_lds = reinterpret_cast<const float*>(smem + G::SC_BIAS);
+  const bool has_bias = p.bias != nullptr;
+  const int lr = lane & 31, lq = 4 * (lane >> 5);
+  float sa[G::FM];
+  static_for<0, G::FM>([&](auto i) { sa[i] = MODE != EPI_INT ? sa_lds[wr * G::WM + 32 * i + lr] : 0.0f; });
+  // output bits of the 4 columns of quad g of block (i, j): 4 words (4-byte
+  // outputs) or 2 packed words (2-byte outputs) in w[0..]
+  auto quad_bits = [&](auto i, auto j, auto g, const f32x4& sb4, const f32x4& bv4, uint32_t (&w)[4]) {
+    constexpr int r0 = 4 * decltype(g)::value;
+    if constexpr (MODE == EPI_INT) {
+      static_for<0, 4>([&](auto c) { w[c] = static_cast<uint32_t>(acc[i][j][r0 + decltype(c)::value]); });
+    } else {
+      float v[4];
+      static_for<0, 4>([&](auto c) {
+        constexpr int C = decltype(c)::value;
+        v[C] = epi_value<OUT, MODE>(acc[i][j][r0 + C], sa[i], sb4[C], bv4[C], has_bias);
+      });
+      if constexpr (out_size<OUT>() == 4) {
+        static_for<0, 4>([&](auto c) { w[c] = __float_as_uint(v[c]); });
+      } else {
+        w[0] = pack2<OUT>(v[0], v[1]);
+        w[1] = pack2<OUT>(v[2], v[3]);
+      }
+    }
+  };
+  auto params = [&](int c0, f32x4& sb4, f32x4& bv4) {
+    sb4 = f32x4{0, 0, 0, 0};
+    bv4 = f32x4{0, 0, 0, 0};
+    if constexpr (MODE != EPI_INT) {
+      sb4 = col4(sb_lds, c0);
+      if (has_bias) bv4 = col4(bv_lds, c0);
+    }
+  };
+
+  constexpr int ES = out_size<OUT>();
+  const bool full = m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((static_cast<int64_t>(p.N) * ES) % 16) == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+  if (full) {
+    // PF blocks of 32 rows per pass through the wave's staging region
+    constexpr int ROWB = G::WN * ES + 16;  // padded LDS row pitch
+    constexpr int REGION = G::RING / G::NW;
+    constexpr int PF = (G::FM * 32 * ROWB <= REGION) ? G::FM : (G::FM / 2 * 32 * ROWB <= REGION) ? G::FM / 2 : 1;
+    static_assert(PF * 32 * ROWB <= REGION && G::FM % PF == 0, "epilogue staging does not fit");
+    constexpr int CHUNKS = G::WN * ES / 16;  // 16-byte chunks per row
+    char* region = smem + wave * REGION;
+    char* out = static_cast<char*>(p.out);
+    static_for<0, G::FM / PF>([&](auto pass) {
+      static_for<0, G::FN>([&](auto j) {
+        static_for<0, 4>([&](auto g) {
+          const int c0 = 32 * decltype(j)::value + 8 * decltype(g)::value + lq;  // wave sub-tile column
+          f32x4 sb4, bv4;
+          params(wc * G::WN + c0, sb4, bv4);
+          static_for<0, PF>([&](auto ii) {
+            constexpr int i = decltype(pass)::value * PF + decltype(ii)::value;
+            uint32_t w[4];
+            quad_bits(std::integral_constant<int, i>{}, j, g, sb4, bv4, w);
+            char* dst = region + (decltype(ii)::value * 32 + lr) * ROWB + c0 * ES;
+            if constexpr (ES == 4) *reinterpret_cast<i32x4*>(dst) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            else *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
+          });
+        });
+      });
+      // LDS accesses of one wave complete in order; the reads below see the writes.
+      constexpr int TOTAL = PF * 32 * CHUNKS;
+      static_assert(TOTAL % 64 == 0, "whole chunk rounds per lane");
+#pragma unroll
+      for (int c0 = 0; c0 < TOTAL; c0 += 64) {
+        const int c = c0 + lane;
+        const int rr = c / CHUNKS, cc = c - rr * CHUNKS;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
+        const int64_t grow = m0 + wr * G::WM + decltype(pass)::value * PF * 32 + rr;
+        const int64_t gcol = n0 + wc * G::WN;
+        *reinterpret_cast<i32x4*>(out + (grow * p.N + gcol) * ES + cc * 16) = v;
+      }
+    });
+  } else {
+    static_for<0, G::FN>([&](auto j) {
+      static_for<0, 4>([&](auto g) {
+        const int c0 = wc * G::WN + 32 * decltype(j)::value + 8 * decltype(g)::value + lq;  // tile column
+        f32x4 sb4, bv4;
+        params(c0, sb4, bv4);
+        static_for<0, G::FM>([&](auto i) {
+          const int row = m0 + wr * G::WM + 32 * decltype(i)::value + lr;
+          uint32_t w[4];
+          quad_bits(i, j, g, sb4, bv4, w);
+          if (row < p.M) {
+            static_for<0, 4>([&](auto c) {
+              constexpr int C = decltype(c)::value;
+              const int col = n0 + c0 + C;
+              const uint32_t bits = ES == 4 ? w[C] : (w[C / 2] >> (16 * (C & 1))) & 0xffffu;
+              if (col < p.N) store_elem<OUT>(p.out, static_cast<int64_t>(row) * p.N + col, bits);
+            });
+          }
+        });
+      });
+    });
+  }
 }
 
 template <typename G, int OUT, int MODE>
@@ -703,9 +769,18 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
   static_for<0, G::FM>([&](auto i) {
     static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
   });
+  auto park = [&]() {
+    if constexpr (MODE != EPI_INT) {
+      if (tid < G::BM) reinterpret_cast<float*>(smem + G::SC_A)[tid] = ep.sa;
+      if (tid < G::BN) {
+        reinterpret_cast<float*>(smem + G::SC_B)[tid] = ep.sb;
+        reinterpret_cast<float*>(smem + G::SC_BIAS)[tid] = bias_value(ep.bias, p.bias_dtype);
+      }
+    }
+  };
   pp_mainloop<G>(acc, smem, reinterpret_cast<const char*>(p.a), reinterpret_cast<const char*>(p.w), voff,
-                 p.K / G::KS, wave, lane);
-  i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
+                 p.K / G::KS, wave, lane, park);
+  pp_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane);
 }
 
 __device__ __forceinline__ float silu(float g) {
@@ -715,14 +790,17 @@ __device__ __forceinline__ float silu(float g) {
 }
 
 // Grouped (MoE) INT8 GEMM on the ping-pong main loop. The grid walks the
-// device tile table (tiles_max 256-row tiles x ceil(N / 192) column tiles):
-// tile t = {expert e (< 0: none), first routed row m0, end of the expert's
-// valid rows}; tile 0's spare field holds the number of tiles in use. A row of routed row r is row_token[r] (or r), W and b_scale
-// start at expert e. Epilogues (v = f32(acc) * (sa[r] * sb[e, n]), order F):
+// device tile table (tiles_max tiles of G::BM routed rows x ceil(N / G::BN)
+// column tiles): tile t = {expert e (< 0: none), first routed row m0, end of
+// the expert's valid rows}; tile 0's spare field holds the number of tiles in
+// use. A row of routed row r is row_token[r] (or r), W and b_scale start at
+// expert e. Epilogues (v = f32(acc) * (sa[r] * sb[e, n]), order F):
 //   QG_MOE_EPI_I32       out int32 [M, N] = acc (routed rows)
 //   QG_MOE_EPI_SILU_MUL  columns 32 b .. 32 b + 15 are the gate and
 //                        32 b + 16 .. 32 b + 31 the up rows of features
 //                        16 b .. 16 b + 15: out bf16 [M, N / 2] = silu(g) * u
+//                        (in the transposed layout the gate and up values of
+//                        a feature sit in the same lane, registers r and r + 8)
 //   QG_MOE_EPI_ROUTE     out bf16 [slots, N] row row_slot[r] = v * row_weight[r]
 template <typename G, int MOE>
 __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
@@ -785,27 +863,29 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
   static_for<0, G::FM>([&](auto i) {
     static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
   });
-  pp_mainloop<G>(acc, smem, reinterpret_cast<const char*>(p.a),
-                 reinterpret_cast<const char*>(p.w) + static_cast<int64_t>(e) * p.w_estride, voff, p.K / G::KS,
-                 wave, lane);
-
-  // ---- epilogue: parameters through LDS (the rings are free now) ------------
-  // row weights / output rows sit after the GEMM's own parameter area
+  // row scales, column scales, row weights and output rows (the latter two
+  // after the GEMM's own parameter area)
   float* sa_lds = reinterpret_cast<float*>(smem + G::SC_A);
   float* sb_lds = reinterpret_cast<float*>(smem + G::SC_B);
   float* rw_lds = reinterpret_cast<float*>(smem + G::LDS_BYTES);
   int* dst_lds = reinterpret_cast<int*>(smem + G::LDS_BYTES + G::BM * 4);
-  if (tid < G::BM) {
-    sa_lds[tid] = ld_sa;
-    rw_lds[tid] = ld_rw;
-    dst_lds[tid] = ld_dst;
-  }
-  if (tid < G::BN) sb_lds[tid] = ld_sb;
-  __syncthreads();
-  const int lh = 4 * (lane >> 5);
-  const int lcol = lane & 31;
+  auto park = [&]() {
+    if (tid < G::BM) {
+      sa_lds[tid] = ld_sa;
+      rw_lds[tid] = ld_rw;
+      dst_lds[tid] = ld_dst;
+    }
+    if (tid < G::BN) sb_lds[tid] = ld_sb;
+  };
+  pp_mainloop<G>(acc, smem, reinterpret_cast<const char*>(p.a),
+                 reinterpret_cast<const char*>(p.w) + static_cast<int64_t>(e) * p.w_estride, voff, p.K / G::KS,
+                 wave, lane, park);
+
+  // ---- epilogue -------------------------------------------------------------
+  const int lr = lane & 31, lq = 4 * (lane >> 5);
   // bf16 outputs whose rows take whole 16-byte chunks are staged per wave in
-  // LDS and written as row chunks; int32 (test) output goes element-wise
+  // its part of the rings and written as row chunks; int32 (test) output goes
+  // element-wise
   constexpr bool STAGED = MOE != QG_MOE_EPI_I32;
   constexpr int OCOLS = MOE == QG_MOE_EPI_SILU_MUL ? G::WN / 2 : G::WN;  // output columns per wave row
   constexpr int ROWB = OCOLS * 2 + 16;
@@ -815,52 +895,87 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
   const bool staged = STAGED && (out_cols % 8) == 0 && (p.out_sm % 8) == 0 &&
                       (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
   char* region = smem + wave * (G::RING / G::NW);
-  float sbv[G::FN];
-  static_for<0, G::FN>([&](auto j) { sbv[j] = sb_lds[wc * G::WN + j * 32 + lcol]; });
+  float sa[G::FM], rwv[G::FM];
   static_for<0, G::FM>([&](auto i) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      // rows 32 i + 8 q + lh + (0..3) of the wave sub-tile: aligned LDS vectors
-      const int rw0 = 32 * i + 8 * q + lh;
-      const f32x4 sa4 = *reinterpret_cast<const f32x4*>(sa_lds + wr * G::WM + rw0);
-      f32x4 rw4 = {0, 0, 0, 0};
-      if constexpr (MOE == QG_MOE_EPI_ROUTE) rw4 = *reinterpret_cast<const f32x4*>(rw_lds + wr * G::WM + rw0);
-      static_for<0, G::FN>([&](auto j) {
-        const int cl = wc * G::WN + j * 32 + lcol;  // tile column of this lane
-        const int n = n0 + cl;
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const int rw_ = rw0 + r4;          // row in the wave sub-tile
-          const int rl = wr * G::WM + rw_;   // tile row
-          const int row = m0 + rl;
-          const int32_t a = acc[i][j][4 * q + r4];
-          if constexpr (MOE == QG_MOE_EPI_I32) {
-            if (row < m_end && n < p.N) static_cast<int32_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + n] = a;
+    const int rl = wr * G::WM + 32 * decltype(i)::value + lr;
+    sa[i] = sa_lds[rl];
+    rwv[i] = MOE == QG_MOE_EPI_ROUTE ? rw_lds[rl] : 0.0f;
+  });
+  static_for<0, G::FN>([&](auto j_c) {
+    constexpr int j = decltype(j_c)::value;
+    if constexpr (MOE == QG_MOE_EPI_I32) {
+      static_for<0, 4>([&](auto g_c) {
+        constexpr int g = decltype(g_c)::value;
+        static_for<0, G::FM>([&](auto i) {
+          const int row = m0 + wr * G::WM + 32 * decltype(i)::value + lr;
+          static_for<0, 4>([&](auto c) {
+            const int n = n0 + wc * G::WN + 32 * j + 8 * g + lq + decltype(c)::value;
+            if (row < m_end && n < p.N)
+              static_cast<int32_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + n] =
+                  acc[i][j][4 * g + decltype(c)::value];
+          });
+        });
+      });
+    } else if constexpr (MOE == QG_MOE_EPI_SILU_MUL) {
+      static_for<0, 2>([&](auto g_c) {
+        constexpr int g = decltype(g_c)::value;
+        const f32x4 sbg = col4(sb_lds, wc * G::WN + 32 * j + 8 * g + lq);
+        const f32x4 sbu = col4(sb_lds, wc * G::WN + 32 * j + 8 * (g + 2) + lq);
+        static_for<0, G::FM>([&](auto i) {
+          float h[4];
+          static_for<0, 4>([&](auto c) {
+            constexpr int C = decltype(c)::value;
+            const float gv = static_cast<float>(acc[i][j][4 * g + C]) * (sa[i] * sbg[C]);
+            const float uv = static_cast<float>(acc[i][j][4 * (g + 2) + C]) * (sa[i] * sbu[C]);
+            h[C] = silu(gv) * uv;
+          });
+          const int rw_ = 32 * decltype(i)::value + lr;  // row in the wave sub-tile
+          const int fl = 16 * j + 8 * g + lq;            // feature in the wave's output columns
+          if (staged) {
+            *reinterpret_cast<u32x2*>(region + rw_ * ROWB + fl * 2) =
+                u32x2{pack2<QG_BF16>(h[0], h[1]), pack2<QG_BF16>(h[2], h[3])};
           } else {
-            const float v = static_cast<float>(a) * (sa4[r4] * sbv[j]);
-            if constexpr (MOE == QG_MOE_EPI_SILU_MUL) {
-              const float u = __shfl_xor(v, 16, 64);  // up value of this gate lane's feature
-              if ((lane & 16) == 0) {
-                const uint16_t bits = f32_to_bf16(silu(v) * u);
-                if (staged) {
-                  *reinterpret_cast<uint16_t*>(region + rw_ * ROWB + (16 * j + (lane & 15)) * 2) = bits;
-                } else if (row < m_end && n < p.N) {
-                  const int feat = ((n0 + wc * G::WN + j * 32) >> 5) * 16 + (lane & 15);
-                  static_cast<uint16_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + feat] = bits;
-                }
-              }
-            } else {
-              const uint16_t bits = f32_to_bf16(v * rw4[r4]);
-              if (staged) {
-                *reinterpret_cast<uint16_t*>(region + rw_ * ROWB + (j * 32 + lcol) * 2) = bits;
-              } else {
-                const int d = dst_lds[rl];
-                if (row < m_end && d >= 0 && d < p.out_rows && n < p.N)
-                  static_cast<uint16_t*>(p.out)[static_cast<int64_t>(d) * p.out_sm + n] = bits;
-              }
+            const int row = m0 + wr * G::WM + rw_;
+            const int f0 = (n0 + wc * G::WN) / 2 + fl;
+            if (row < m_end) {
+              static_for<0, 4>([&](auto c) {
+                if (f0 + decltype(c)::value < out_cols)
+                  static_cast<uint16_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + f0 + decltype(c)::value] =
+                      f32_to_bf16(h[decltype(c)::value]);
+              });
             }
           }
-        }
+        });
+      });
+    } else {
+      static_for<0, 4>([&](auto g_c) {
+        constexpr int g = decltype(g_c)::value;
+        const int cl = wc * G::WN + 32 * j + 8 * g + lq;  // tile column
+        const f32x4 sb4 = col4(sb_lds, cl);
+        static_for<0, G::FM>([&](auto i) {
+          float y[4];
+          static_for<0, 4>([&](auto c) {
+            constexpr int C = decltype(c)::value;
+            const float v = static_cast<float>(acc[i][j][4 * g + C]) * (sa[i] * sb4[C]);
+            y[C] = v * rwv[i];
+          });
+          const int rw_ = 32 * decltype(i)::value + lr;
+          if (staged) {
+            *reinterpret_cast<u32x2*>(region + rw_ * ROWB + (32 * j + 8 * g + lq) * 2) =
+                u32x2{pack2<QG_BF16>(y[0], y[1]), pack2<QG_BF16>(y[2], y[3])};
+          } else {
+            const int rl = wr * G::WM + rw_;
+            const int d = dst_lds[rl];
+            if (m0 + rl < m_end && d >= 0 && d < p.out_rows) {
+              static_for<0, 4>([&](auto c) {
+                const int n = n0 + cl + decltype(c)::value;
+                if (n < p.N)
+                  static_cast<uint16_t*>(p.out)[static_cast<int64_t>(d) * p.out_sm + n] =
+                      f32_to_bf16(y[decltype(c)::value]);
+              });
+            }
+          }
+        });
       });
     }
   });
@@ -889,10 +1004,8 @@ hipError_t launch_tile(const I8GemmArgs& p, hipStream_t stream) {
   const int blocks = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
   if constexpr (G::NW == 4)
     hipLaunchKernelGGL((k_i8_gemm<G, WPE, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
-  else if (kI8PingPong)
-    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
   else
-    hipLaunchKernelGGL((k_i8_gemm_jit<G, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
+    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -171,6 +171,45 @@ def test_int8_shapes_tails(cuda, m, n, k):
     assert np.array_equal(f16_bits(out), ref.view(np.int16))
 
 
+def _bits(x, out):
+    """Storage bits of a GPU output tensor / of oracle fp32 values (as uint)."""
+    if isinstance(x, torch.Tensor):
+        x = x.detach().cpu()
+        return x.view(torch.int32).numpy().view(np.uint32) if out == "f32" else x.view(torch.int16).numpy().view(np.uint16)
+    enc = o.encode(x, out)
+    return enc.view(np.uint32) if out == "f32" else enc.view(np.uint16)
+
+
+@pytest.mark.parametrize("m,n,k", [(4000, 3000, 384), (4096, 3072, 128), (4096, 3072, 256), (3841, 2881, 512)])
+def test_int8_pingpong_edges_and_epilogues(cuda, m, n, k):
+    """Shapes of >= 192 tiles of 256 x 192, i.e. the 8-wave ping-pong kernel:
+    edge tiles in both dimensions, one and two K stages, rows whose byte length
+    is not a multiple of 16 (element-wise stores). int32 and every epilogue
+    order / output dtype bit-exact against the oracle."""
+    from rdna2_ops.int8_gemm import int8_gemm_dequant, int8_matmul
+    case(f"int8 ping-pong {m}x{n}x{k}")
+    g = torch.Generator().manual_seed(m + 3 * n + 7 * k)
+    a = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    sa = torch.rand(m, generator=g) * 0.02 + 0.001
+    sb = torch.rand(n, generator=g) * 0.02 + 0.001
+    bias = torch.randn(n, generator=g)
+    acc_o = o.int8_matmul(a.numpy(), np.ascontiguousarray(w.numpy().T))
+    ag, wg, sag, sbg = a.to(cuda), w.to(cuda), sa.to(cuda), sb.to(cuda)
+    assert np.array_equal(int8_matmul(ag, wg.T).cpu().numpy(), acc_o)
+    dts = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+    for out, bias_dt, kw in (("f16", "f16", {}), ("bf16", "bf16", {}), ("f32", "f32", {}), ("bf16", None, {}),
+                             ("f16", "f16", {"rounding": "fused"}), ("bf16", "bf16", {"epilogue_order": "eager"})):
+        bt = None if bias_dt is None else bias.to(dts[bias_dt])
+        got = int8_gemm_dequant(ag, wg.T, sag, sbg, None if bt is None else bt.to(cuda), out_dtype=dts[out], **kw)
+        bv = None if bt is None else bt.float().numpy()
+        if kw.get("epilogue_order") == "eager":
+            ref = o.epilogue_e(acc_o, sa.numpy(), sb.numpy(), bv, out=out)
+        else:
+            ref = o.epilogue_f(acc_o, sa.numpy(), sb.numpy(), bv, out=out, fused=kw.get("rounding") == "fused")
+        assert np.array_equal(_bits(got, out), _bits(ref, out)), (out, bias_dt, kw)
+
+
 def test_int8_extreme_values(cuda):
     """All -128 operands at K = 131071 reach the int32 bound exactly; -128/127
     mixes exercise sign handling."""

@@ -275,12 +275,15 @@ int qg_moe_sizes(int64_t tokens, int n_experts, int top_k, int pad, int64_t* row
  * Routed rows grouped by expert (expert 0 first), each expert's segment
  * padded to a multiple of pad rows: row_token (token, -1 for padding),
  * row_weight (0 for padding), row_slot (t * top_k + k, -1 for padding), each
- * [rows_max]; tokens are in arbitrary order inside a segment.
+ * [rows_max]; inside a segment the rows are in slot order (t * top_k + k
+ * ascending), so the dispatch is deterministic; rows past the last segment
+ * are padding too.
  * tiles int32 [tiles_max][4] = {expert (-1: unused), first row, end of the
  * expert's valid rows, 0}; tiles[0][3] = number of tiles in use (the used
  * tiles come first). counts: int32 workspace [QG_MOE_COUNTS_PER_EXPERT *
- * n_experts]: per-expert counts and segment offsets first, then the sort's
- * per-block histograms. */
+ * n_experts]: per-expert counts, segment offsets and first tiles, then the
+ * sort's per-block histograms. Two launches, no host synchronisation and no
+ * memset (capturable in a graph). */
 int qg_moe_dispatch(const float* logits, int64_t l_sm, int64_t tokens, int n_experts, int top_k, int pad,
                     int32_t* experts, float* weights, int32_t* counts, int32_t* row_token,
                     float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,

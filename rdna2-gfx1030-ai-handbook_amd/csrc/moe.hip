@@ -2,19 +2,23 @@
 // 4; the reference repository has no MoE kernel). The grouped INT8 GEMM that
 // runs between dispatch and combine is k_i8_moe_pp in int8_gemm.hip.
 //
-//   init     zero the per-expert counters, mark every routed row as padding
-//            and every tile as empty (no memset node: safe under graph capture)
+// The dispatch is a stable counting sort of the tokens * top_k routed slots
+// by expert, in two launches over sort blocks of tb consecutive tokens
+// (tb * top_k slots, at most kMaxSortBlocks blocks):
 //   route    one wave per token, lane e = expert e: softmax over the experts
-//            in fp32 and the top_k experts by logit (ties: lower index)
-//   count    a stable counting sort of the tokens * top_k slots in three
-//   plan     steps: per-block expert histograms (blocks of kSortBlock slots,
-//   scatter  LDS atomics); one workgroup turns them into per-expert segments
-//            padded to `pad` rows, each block's first row per expert and the
-//            table of tile_rows-row tiles of the grouped GEMM (tile 0's spare
-//            field holds the number of tiles in use); then every slot's row =
-//            its block's base + earlier waves of the block + its rank among
-//            equal experts of its 64-slot step (six ballots). Rows inside a
-//            segment are in slot order, so the dispatch is deterministic
+//            in fp32 and the top_k experts by logit (ties: lower index); the
+//            block counts its slots per expert (LDS atomics) into its
+//            histogram
+//   scatter  every block derives the plan from all histograms: expert
+//            counts, segments padded to `pad` rows (wave-wide scans, lane =
+//            expert), its own first row per expert; block 0 writes the table
+//            of tile_rows-row tiles of the grouped GEMM (tile 0's spare field
+//            holds the number of tiles in use, unused tiles are empty); the
+//            padding rows and the rows past the last segment are marked empty
+//            (no memset node: safe under graph capture). Then every slot's
+//            row = its block's first row + earlier waves of the block + its
+//            rank among equal experts of its 64-slot step (six ballots). Rows
+//            inside a segment are in slot order: the dispatch is deterministic
 //   combine  out[t] = bf16(sum over k of y[t * top_k + k]) in k order (fp32)
 #include "qg_common.h"
 #include "qg_internal.h"
@@ -23,24 +27,13 @@ namespace qg {
 
 namespace {
 
-constexpr int kSortBlock = 1024;      // slots per sort block (at least)
 constexpr int kMaxSortBlocks = 256;
+constexpr int kRouteWaves = 16;  // waves (tokens in flight) per routing block
 
-__global__ __launch_bounds__(256) void k_moe_init(MoeDispatchArgs p) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < p.rows_max; i += stride) {
-    p.row_token[i] = -1;
-    p.row_slot[i] = -1;
-    p.row_weight[i] = 0.0f;
-  }
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < p.tiles_max; i += stride) {
-    p.tiles[4 * i] = -1;
-    p.tiles[4 * i + 1] = 0;
-    p.tiles[4 * i + 2] = 0;
-    p.tiles[4 * i + 3] = 0;
-  }
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < 3 * p.E; i += 256) p.counts[i] = 0;
+// Tokens per sort block: blocks of tb tokens, at most kMaxSortBlocks of them.
+__host__ __device__ __forceinline__ int sort_block_tokens(int T) {
+  const int tb = ceil_div(T, kMaxSortBlocks);
+  return tb > 0 ? tb : 1;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -49,30 +42,53 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void k_moe_route(MoeDispatchArgs p) {
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(v, o, kWave);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+// counts layout: [0, E) counts, [E, 2E) segment offsets, [2E, 3E) first tile
+// of each expert, then [kMaxSortBlocks][E] per-block histograms (the
+// workspace holds (3 + 256) E ints).
+__global__ __launch_bounds__(kRouteWaves * 64) void k_moe_route(MoeDispatchArgs p) {
 #pragma clang fp contract(off)
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= p.T) return;  // whole wave
-  const int e = threadIdx.x & 63;
+  __shared__ int hist[64];
+  const int tb = sort_block_tokens(p.T);
+  const int b = blockIdx.x;
+  if (threadIdx.x < 64) hist[threadIdx.x] = 0;
+  __syncthreads();
+  const int e = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bool live = e < p.E;
-  const float l = live ? p.logits[static_cast<int64_t>(t) * p.l_sm + e] : -__builtin_inff();
-  const float mx = wave_max(l);
-  const float ex = live ? __builtin_amdgcn_exp2f((l - mx) * 1.4426950408889634f) : 0.0f;
-  const float prob = __fdiv_rn(ex, wave_sum(ex));
-  bool taken = false;
-  for (int k = 0; k < p.top_k; ++k) {
-    const bool cand_ok = live && !taken;
-    const float cand = cand_ok ? l : -__builtin_inff();
-    const float mk = wave_max(cand);
-    uint64_t win = __ballot(cand_ok && cand == mk);
-    if (win == 0) win = __ballot(cand_ok);  // NaN logits: lowest free expert
-    const int w = static_cast<int>(__builtin_ctzll(win));
-    if (e == w) {
-      taken = true;
-      p.experts[static_cast<int64_t>(t) * p.top_k + k] = e;
-      p.weights[static_cast<int64_t>(t) * p.top_k + k] = prob;
+  const int t_end = min(p.T, (b + 1) * tb);
+  for (int t = b * tb + wave; t < t_end; t += kRouteWaves) {
+    const float l = live ? p.logits[static_cast<int64_t>(t) * p.l_sm + e] : -__builtin_inff();
+    const float mx = wave_max(l);
+    const float ex = live ? __builtin_amdgcn_exp2f((l - mx) * 1.4426950408889634f) : 0.0f;
+    const float prob = __fdiv_rn(ex, wave_sum(ex));
+    bool taken = false;
+    for (int k = 0; k < p.top_k; ++k) {
+      const bool cand_ok = live && !taken;
+      const float cand = cand_ok ? l : -__builtin_inff();
+      const float mk = wave_max(cand);
+      uint64_t win = __ballot(cand_ok && cand == mk);
+      if (win == 0) win = __ballot(cand_ok);  // NaN logits: lowest free expert
+      const int w = static_cast<int>(__builtin_ctzll(win));
+      if (e == w) {
+        taken = true;
+        p.experts[static_cast<int64_t>(t) * p.top_k + k] = e;
+        p.weights[static_cast<int64_t>(t) * p.top_k + k] = prob;
+        atomicAdd(&hist[e], 1);
+      }
     }
   }
+  __syncthreads();
+  if (threadIdx.x < p.E) p.counts[3 * p.E + b * p.E + threadIdx.x] = hist[threadIdx.x];
 }
 
 // Lanes of the wave whose value of e (< 64) equals this lane's, among the
@@ -87,96 +103,137 @@ __device__ __forceinline__ uint64_t match_expert(int e, uint64_t valid) {
   return m;
 }
 
-// counts layout: [0, E) counts, [E, 2E) segment offsets, [2E, 3E) spare,
-// then [kMaxSortBlocks][E] per-block histograms / first rows (the workspace
-// holds (3 + 256) E ints).
-__host__ __device__ __forceinline__ int sort_block_size(int slots) {
-  const int b = (ceil_div(slots, kMaxSortBlocks) + 255) / 256 * 256;
-  return b > kSortBlock ? b : kSortBlock;
-}
-
-__global__ __launch_bounds__(256) void k_moe_count(MoeDispatchArgs p) {
-  __shared__ int hist[64];
-  const int slots = p.T * p.top_k;
-  const int bs = sort_block_size(slots);
-  const int b = blockIdx.x;
-  if (threadIdx.x < 64) hist[threadIdx.x] = 0;
-  __syncthreads();
-  const int s_end = min(slots, (b + 1) * bs);
-  for (int s = b * bs + threadIdx.x; s < s_end; s += 256) atomicAdd(&hist[p.experts[s]], 1);
-  __syncthreads();
-  if (threadIdx.x < p.E) p.counts[3 * p.E + b * p.E + threadIdx.x] = hist[threadIdx.x];
-}
-
-// sum over blocks b' in [0, nb) of the block histograms of expert (tid & 63),
-// four threads per expert (tid >> 6 picks b' modulo 4), reduced in LDS
-__device__ __forceinline__ int sum_block_hist(const int* bh, int E, int nb, int (*part)[64]) {
-  const int e = threadIdx.x & 63, q = threadIdx.x >> 6;
-  int c = 0;
-  if (e < E)
-    for (int b = q; b < nb; b += 4) c += bh[b * E + e];
-  part[q][e] = c;
-  __syncthreads();
-  const int r = part[0][e] + part[1][e] + part[2][e] + part[3][e];
-  __syncthreads();
-  return r;
-}
-
-__global__ __launch_bounds__(256) void k_moe_plan(MoeDispatchArgs p) {
-  __shared__ int part[4][64];
-  __shared__ int off[64], cnt[64];
-  const int e = threadIdx.x;
-  const int slots = p.T * p.top_k;
-  const int nb = ceil_div(slots, sort_block_size(slots));
-  const int c = sum_block_hist(p.counts + 3 * p.E, p.E, nb, part);
-  if (e < 64) cnt[e] = c;
-  __syncthreads();
-  if (e == 0) {
-    int o = 0, tl = 0;
-    for (int i = 0; i < p.E; ++i) {
-      const int padded = (cnt[i] + p.pad - 1) / p.pad * p.pad;
-      off[i] = o;
-      o += padded;
-      tl += (padded + p.tile_rows - 1) / p.tile_rows;
-    }
-    p.tiles[3] = min(tl, p.tiles_max);  // tiles in use (tile 0's spare field)
-  }
-  __syncthreads();
-  if (e < p.E) {
-    p.counts[e] = cnt[e];
-    p.counts[p.E + e] = off[e];
-    int tile0 = 0;
-    for (int i = 0; i < e; ++i) tile0 += ((cnt[i] + p.pad - 1) / p.pad * p.pad + p.tile_rows - 1) / p.tile_rows;
-    const int padded = (cnt[e] + p.pad - 1) / p.pad * p.pad;
-    const int nt = (padded + p.tile_rows - 1) / p.tile_rows;
-    for (int j = 0; j < nt && tile0 + j < p.tiles_max; ++j) {
-      int* td = p.tiles + 4 * (tile0 + j);
-      td[0] = e;
-      td[1] = off[e] + j * p.tile_rows;
-      td[2] = off[e] + cnt[e];
-    }
-  }
-}
-
+// Every workgroup (256 threads, one per sort block) first derives the whole
+// plan from the sort blocks' histograms [nb][E]: thread (q = tid >> 6,
+// e = tid & 63) sums expert e's entries of blocks q, q + 4, ... (all, and
+// those before this block); wave 0 then turns the expert counts into padded
+// segments and tiles with wave-wide scans (lane = expert). Block 0 writes the
+// counts, offsets and the tile table; the padding rows of expert e are
+// marked empty by block e mod nb, the rows past the last segment by all
+// blocks in turn. Then the block scatters its slots.
 __global__ __launch_bounds__(256) void k_moe_scatter(MoeDispatchArgs p) {
-  __shared__ int part[4][64];
   __shared__ int hist[4][64];
+  __shared__ int part[4][64], prior[4][64];
+  __shared__ int seg[64], cnt_s[64], pad_s[64], tile0_s[64], ntile_s[64];
+  __shared__ int totals[2];  // rows and tiles of all segments
   const int slots = p.T * p.top_k;
-  const int bs = sort_block_size(slots);
+  const int tb = sort_block_tokens(p.T);
+  const int nb = ceil_div(p.T, tb);  // 0 without tokens (one workgroup runs)
+  const int nbl = nb > 0 ? nb : 1;
   const int b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // wave w takes slots [b bs + w bs/4, b bs + (w+1) bs/4)
-  const int per_wave = bs / 4;
-  const int s_begin = b * bs + wave * per_wave, s_end = min(slots, s_begin + per_wave);
-  // this block's first row per expert: segment offset + earlier blocks
-  const int before = sum_block_hist(p.counts + 3 * p.E, p.E, b, part);
+  const int* bh = p.counts + 3 * p.E;
+  // wave w takes slots [b bs + w pw, b bs + (w+1) pw) of the block; the first
+  // 64-slot step's experts and weights are fetched before the plan
+  const int bs = tb * p.top_k;
+  const int pw = ceil_div(bs, 4);
+  const int blk_end = min(slots, (b + 1) * bs);
+  const int s_begin = min(blk_end, b * bs + wave * pw), s_end = min(blk_end, s_begin + pw);
+  const bool ok0 = s_begin + lane < s_end;
+  const int e0 = ok0 ? p.experts[s_begin + lane] : 0;
+  const float w0 = ok0 ? p.weights[s_begin + lane] : 0.0f;
+
+  // ---- plan ------------------------------------------------------------------
+  {
+    const int e = lane, q = wave;
+    int tot = 0, bef = 0;
+    if (e < p.E) {
+      // kBatch independent loads in flight per round (a dependent sum would
+      // wait one memory latency per block)
+      constexpr int kBatch = 32;
+      for (int bb0 = q; bb0 < nb; bb0 += 4 * kBatch) {
+        int v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int bb = bb0 + 4 * u;
+          v[u] = bb < nb ? bh[bb * p.E + e] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          tot += v[u];
+          if (bb0 + 4 * u < b) bef += v[u];
+        }
+      }
+    }
+    part[q][e] = tot;
+    prior[q][e] = bef;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int e = lane;
+    const int cnt = e < p.E ? part[0][e] + part[1][e] + part[2][e] + part[3][e] : 0;
+    const int padded = (cnt + p.pad - 1) / p.pad * p.pad;
+    const int nt = (padded + p.tile_rows - 1) / p.tile_rows;
+    const int off_inc = wave_inclusive_scan(padded), t_inc = wave_inclusive_scan(nt);
+    seg[e] = off_inc - padded;
+    cnt_s[e] = cnt;
+    pad_s[e] = padded;
+    tile0_s[e] = t_inc - nt;
+    ntile_s[e] = nt;
+    if (e == 63) {
+      totals[0] = off_inc;
+      totals[1] = t_inc;
+    }
+    if (b == 0 && e < p.E) {
+      p.counts[e] = cnt;
+      p.counts[p.E + e] = off_inc - padded;
+      p.counts[2 * p.E + e] = t_inc - nt;
+    }
+  }
+  __syncthreads();
+  const int rows_used = totals[0];
+  const int tiles_used = min(totals[1], p.tiles_max);
+  if (b == 0) {
+    // thread (q, e) writes tiles q, q + 4, ... of expert e; then the unused ones
+    const int e = lane;
+    if (e < p.E) {
+      for (int j = wave; j < ntile_s[e]; j += 4) {
+        const int ti = tile0_s[e] + j;
+        if (ti < p.tiles_max) {
+          int* td = p.tiles + 4 * ti;
+          td[0] = e;
+          td[1] = seg[e] + j * p.tile_rows;
+          td[2] = seg[e] + cnt_s[e];
+          td[3] = ti == 0 ? tiles_used : 0;
+        }
+      }
+    }
+    for (int ti = tiles_used + threadIdx.x; ti < p.tiles_max; ti += 256) {
+      int* td = p.tiles + 4 * ti;
+      td[0] = -1;
+      td[1] = 0;
+      td[2] = 0;
+      td[3] = ti == 0 ? tiles_used : 0;
+    }
+  }
+  {
+    const int e = lane;
+    if (e < p.E && e % nbl == b) {
+      for (int r = seg[e] + cnt_s[e] + wave; r < seg[e] + pad_s[e]; r += 4) {
+        if (r < p.rows_max) {
+          p.row_token[r] = -1;
+          p.row_slot[r] = -1;
+          p.row_weight[r] = 0.0f;
+        }
+      }
+    }
+  }
+  for (int r = rows_used + b * 256 + threadIdx.x; r < p.rows_max; r += nbl * 256) {
+    p.row_token[r] = -1;
+    p.row_slot[r] = -1;
+    p.row_weight[r] = 0.0f;
+  }
+
+  // ---- scatter ----------------------------------------------------------------
   hist[wave][lane] = 0;
   __syncthreads();
-  for (int s = s_begin + lane; s < s_end; s += 64) atomicAdd(&hist[wave][p.experts[s]], 1);
+  if (ok0) atomicAdd(&hist[wave][e0], 1);
+  for (int s = s_begin + 64 + lane; s < s_end; s += 64) atomicAdd(&hist[wave][p.experts[s]], 1);
   __syncthreads();
   if (threadIdx.x < p.E) {
     const int e = threadIdx.x;
-    int base = p.counts[p.E + e] + before;
+    // the block's first row for expert e, then the earlier waves' slots
+    int base = seg[e] + prior[0][e] + prior[1][e] + prior[2][e] + prior[3][e];
     for (int w = 0; w < 4; ++w) {
       const int h = hist[w][e];
       hist[w][e] = base;
@@ -188,8 +245,8 @@ __global__ __launch_bounds__(256) void k_moe_scatter(MoeDispatchArgs p) {
   for (int s0 = s_begin; s0 < s_end; s0 += 64) {
     const int s = s0 + lane;
     const bool ok = s < s_end;
-    const int e = ok ? p.experts[s] : 0;
-    const float w = ok ? p.weights[s] : 0.0f;
+    const int e = s0 == s_begin ? e0 : (ok ? p.experts[s] : 0);
+    const float w = s0 == s_begin ? w0 : (ok ? p.weights[s] : 0.0f);
     const uint64_t same = match_expert(e, __ballot(ok));
     const int pos = hist[wave][e] + __builtin_popcountll(same & lower);
     if (ok && pos >= 0 && pos < p.rows_max) {
@@ -245,18 +302,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(const uint16_t* y, int T, i
 
 hipError_t launch_moe_dispatch(const MoeDispatchArgs& p, hipStream_t stream) {
   if (p.E > 64) return hipErrorInvalidValue;
-  const int64_t init_items = p.rows_max > p.tiles_max ? p.rows_max : p.tiles_max;
-  int64_t blocks = ceil_div<int64_t>(init_items, 256);
-  if (blocks < 1) blocks = 1;
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(k_moe_init, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p);
-  if (p.T == 0) return hipGetLastError();
-  hipLaunchKernelGGL(k_moe_route, dim3(static_cast<unsigned>(ceil_div(p.T, 4))), dim3(256), 0, stream, p);
-  const int slots = p.T * p.top_k;
-  const int nb = ceil_div(slots, sort_block_size(slots));  // <= kMaxSortBlocks
-  hipLaunchKernelGGL(k_moe_count, dim3(static_cast<unsigned>(nb)), dim3(256), 0, stream, p);
-  hipLaunchKernelGGL(k_moe_plan, dim3(1), dim3(256), 0, stream, p);  // 4 threads per expert
-  hipLaunchKernelGGL(k_moe_scatter, dim3(static_cast<unsigned>(nb)), dim3(256), 0, stream, p);
+  const int nb = p.T > 0 ? ceil_div(p.T, sort_block_tokens(p.T)) : 0;  // <= kMaxSortBlocks
+  if (nb > 0) hipLaunchKernelGGL(k_moe_route, dim3(static_cast<unsigned>(nb)), dim3(kRouteWaves * 64), 0, stream, p);
+  // one workgroup when there are no tokens: it still writes the empty plan
+  hipLaunchKernelGGL(k_moe_scatter, dim3(static_cast<unsigned>(nb > 0 ? nb : 1)), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -132,6 +132,9 @@ def moe_int8_forward(x: torch.Tensor, router_logits: torch.Tensor, weights: MoeI
     if not 1 <= top_k <= e or e > 64:
         raise ValueError("1 <= top_k <= E <= 64 required")
     _lib.require_gfx950(x)
+    if t == 0:  # empty input: empty output, nothing launched
+        out = torch.empty(0, h, dtype=torch.bfloat16, device=x.device)
+        return out if not return_intermediates else (out, {})
     lib = _lib.library()
     dev = x.device
     rows_c, tiles_c = ctypes.c_int64(), ctypes.c_int64()

@@ -39,6 +39,22 @@ def make_case(seed, t, e, h, f, top_k):
     return x, logits, wg, wu, wd
 
 
+def check_tiles(tl, counts, offsets, label=""):
+    """The tile table: every expert segment (padded to 64 rows) cut into
+    MOE_TILE_ROWS-row tiles in expert order, {expert, first row, end of the
+    expert's valid rows}; tile 0's spare field = tiles in use; the rest empty."""
+    from rdna2_ops import _lib
+    tr = _lib.MOE_TILE_ROWS
+    want = []
+    for ei, (c, off) in enumerate(zip(counts, offsets)):
+        padded = (int(c) + 63) // 64 * 64
+        want += [(ei, int(off) + j * tr, int(off) + int(c)) for j in range((padded + tr - 1) // tr)]
+    n = len(want)
+    assert tl[0, 3] == n, label
+    assert np.array_equal(tl[:n, :3], np.array(want, dtype=np.int64).reshape(-1, 3)), label
+    assert (tl[n:, 0] == -1).all() and (tl[n:, 1:3] == 0).all() and (tl[1:, 3] == 0).all(), label
+
+
 def run_and_check(cuda, x, logits, wg, wu, wd, top_k, sample=None, label=""):
     m = mod()
     prep = m.prepare_moe_weights(wg.to(cuda), wu.to(cuda), wd.to(cuda))
@@ -70,6 +86,7 @@ def run_and_check(cuda, x, logits, wg, wu, wd, top_k, sample=None, label=""):
     assert np.array_equal(rt[:rows], rt_o) and np.array_equal(rs[:rows], rs_o), label
     assert (rt[rows:] == -1).all() and (rs[rows:] == -1).all(), label
     assert np.array_equal(rw[rs >= 0], it["weights"].cpu().numpy().reshape(-1)[rs[rs >= 0]])
+    check_tiles(it["tiles"].cpu().numpy(), counts, offsets, label)
     valid = np.argwhere(rs >= 0)[:, 0]
     # x quantization
     xq_o, xs_o = o8.quant_rows(x.float().numpy())
@@ -138,3 +155,33 @@ def test_moe_cfg4_full_size(cuda):
     from rdna2_ops import synthetic
     c = synthetic.cfg4()
     run_and_check(cuda, c.x, c.logits, c.w_gate, c.w_up, c.w_down, c.top_k, sample=384, label="cfg4")
+
+
+def test_moe_dispatch_no_tokens(cuda):
+    """No tokens: the dispatch still writes an empty plan (every row padding,
+    no tile in use, zero counts); the forward returns an empty output."""
+    import ctypes
+    from rdna2_ops import _lib
+    case("moe dispatch without tokens")
+    lib, P = _lib.library(), _lib.ptr
+    e, k, pad = 8, 2, 64
+    rows_c, tiles_c = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(lib.qg_moe_sizes(0, e, k, pad, ctypes.byref(rows_c), ctypes.byref(tiles_c)), "sizes")
+    rows, tiles_n = rows_c.value, tiles_c.value
+    i32 = dict(dtype=torch.int32, device=cuda)
+    counts = torch.full((_lib.MOE_COUNTS_PER_EXPERT * e,), 7, **i32)
+    row_token = torch.full((rows,), 5, **i32)
+    row_slot = torch.full((rows,), 5, **i32)
+    row_weight = torch.full((rows,), 3.0, dtype=torch.float32, device=cuda)
+    tiles = torch.full((tiles_n, 4), 9, **i32)
+    _lib.check(lib.qg_moe_dispatch(None, e, 0, e, k, pad, None, None, P(counts), P(row_token), P(row_weight),
+                                   P(row_slot), rows, P(tiles), tiles_n, _lib.stream_of(counts)), "dispatch")
+    torch.cuda.synchronize()
+    assert (counts[:3 * e].cpu() == 0).all()
+    assert (row_token.cpu() == -1).all() and (row_slot.cpu() == -1).all() and (row_weight.cpu() == 0).all()
+    check_tiles(tiles.cpu().numpy(), np.zeros(e, np.int64), np.zeros(e, np.int64), "no tokens")
+    m = mod()
+    x, logits, wg, wu, wd = make_case(1, 4, e, 128, 128, k)
+    prep = m.prepare_moe_weights(wg.to(cuda), wu.to(cuda), wd.to(cuda))
+    out = m.moe_int8_forward(x[:0].to(cuda), logits[:0].to(cuda), prep, top_k=k)
+    assert out.shape == (0, 128) and out.dtype == torch.bfloat16

@@ -205,6 +205,25 @@ int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m, int64_t k
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * W4A8 linear on the int8 MFMA, integer-exact group sums:
+ *   acc_g[m, n] = sum_{k in group g} a[m, k] * (q[n, k] - zero[n, g])  (exact)
+ *   integer: out int32 [m, n] = sum_g acc_g
+ *   float:   total = 0; for g = 0, 1, ...: total = total + f32(acc_g) * scale[n, g]
+ *            (separate fp32 roundings); out fp32 = total * a_scale[m] (+ bias[n])
+ * Replaces: int4_linear_a8 (int4_weight_gemm_v07.py:476-537) — every method
+ *   (dot4, dot4_split, dot4_words, dot8 :181-353) computes these numbers; with
+ *   prepared != NULL the weights are the caller's centred int8 q - zero [n, k]
+ *   (row stride prepared_sn bytes, method dot4_prepared) and w / zeros are unused.
+ * a: int8 [m, k], row stride a_sm (a multiple of 16 bytes, 16-byte aligned
+ * base); w: the W4 storage above (16-byte aligned); a_scale fp32 [m] (float
+ * output); bias NULL or [n] of bias_dtype; out [m, n] contiguous; m * n < 2^31,
+ * k * 128 * 15 < 2^31 (int4_weight_gemm_v07.py:493). */
+int qg_w4a8_gemm(const int8_t* a, int64_t a_sm, int64_t m, int64_t k, const int32_t* w, int64_t n,
+                 int group_size, int flags, const void* scales, int scales_dtype, const void* zeros,
+                 const int8_t* prepared, int64_t prepared_sn, const float* a_scale, const void* bias,
+                 int bias_dtype, void* out, int integer, void* stream);
+
+/* ---------------------------------------------------------------------------
  * FP8 (OCP e4m3fn / e5m2) weights.
  * ------------------------------------------------------------------------- */
 

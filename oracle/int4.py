@@ -14,14 +14,18 @@ Restates, in numpy on the CPU:
     form that int4_linear_a16 approximates (int4_weight_gemm_v07.py:365-387,
     :540-564; its fp16 rounding of each weight is not part of the oracle);
   * the grouped form of int4_model_switches_v07.py:19-34: per group an exact
-    integer dot product, then the group scale.
+    integer dot product, then the group scale;
+  * W4A8 (int4_linear_a8, int4_weight_gemm_v07.py:476-537): the exact integer
+    product and the fp32 group-scale accumulation in the reference's order.
 
 Pinned by tests/test_oracle_int4.py: the reference's smoke patterns
 (bench_int4_v07.py:89-95: an all-zero row, the 16 integer levels -8..7 and the
 15 levels -7..7, which must round-trip exactly), hand-written words for every
 nibble position in both orders, the rounding-error bound |w - dequant| <= s/2
 for unclipped elements, signed/unsigned storage equivalence and brute-force
-float64 loops for the product.
+float64 loops for the product; W4A8 by scalar loops with one float32 rounding
+per operation, a torch CPU formulation of the reference's grouped reference,
+closed forms and planted mistakes.
 """
 from __future__ import annotations
 
@@ -199,4 +203,59 @@ def w4a16_linear_bruteforce(a, centred, scales, group_size, bias=None):
             for kk in range(k):
                 acc += float(a[i, kk]) * int(centred[j, kk]) * float(scales[j, kk // group_size])
             y[i, j] = acc + (float(bias[j]) if bias is not None else 0.0)
+    return y
+
+
+# ----------------------------------------------------------------- W4A8
+def w4a8_integer(a, centred):
+    """The integer=True result of int4_linear_a8 (int4_weight_gemm_v07.py:476-537):
+    exact int64 [M, N] = sum_k a[m, k] (q - z)[n, k] (float64 BLAS is exact:
+    |sum| <= 128 * 15 * K < 2^53)."""
+    return np.rint(np.asarray(a, np.float64) @ np.asarray(centred, np.float64).T).astype(np.int64)
+
+
+def w4a8_linear(a, centred, scales, a_scale, group_size, bias=None):
+    """The float result of int4_linear_a8 in the reference's declared order
+    (_linear_dot4 int4_weight_gemm_v07.py:200-217, grouped_integer_reference
+    int4_model_switches_v07.py:19-34): per group g the exact integer dot
+    acc_g (exact in fp32: |acc_g| <= 128 * 15 * 128 < 2^24), then in fp32 with
+    a rounding after every operation
+        total = 0; for g ascending: total = total + f32(acc_g) * scale[n, g]
+        y = total * a_scale[m]; y = y + f32(bias[n]).
+    a int8 [M, K]; centred int [N, K] = q - zero; scales [N, K/G] (fp32
+    values); returns fp32 [M, N]."""
+    a64 = np.asarray(a, np.float64)
+    c64 = np.asarray(centred, np.float64)
+    m, k = a64.shape
+    n = c64.shape[0]
+    s = np.asarray(scales, F32)
+    total = np.zeros((m, n), F32)
+    for g in range(k // group_size):
+        sl = slice(g * group_size, (g + 1) * group_size)
+        acc = (a64[:, sl] @ c64[:, sl].T).astype(F32)  # exact
+        total = (total + (acc * s[:, g][None, :]).astype(F32)).astype(F32)
+    y = (total * np.asarray(a_scale, F32).reshape(-1)[:, None]).astype(F32)
+    if bias is not None:
+        y = (y + np.asarray(bias, F32).reshape(1, -1)).astype(F32)
+    return y
+
+
+def w4a8_linear_bruteforce(a, centred, scales, a_scale, group_size, bias=None):
+    """Scalar loops with np.float32 scalars, one rounding per operation; tiny
+    inputs only."""
+    m, k = np.asarray(a).shape
+    n = np.asarray(centred).shape[0]
+    y = np.zeros((m, n), F32)
+    for i in range(m):
+        for j in range(n):
+            total = F32(0)
+            for g in range(k // group_size):
+                acc = 0
+                for kk in range(g * group_size, (g + 1) * group_size):
+                    acc += int(a[i, kk]) * int(centred[j, kk])
+                total = F32(total + F32(F32(acc) * F32(scales[j, g])))
+            v = F32(total * F32(np.asarray(a_scale).reshape(-1)[i]))
+            if bias is not None:
+                v = F32(v + F32(bias[j]))
+            y[i, j] = v
     return y

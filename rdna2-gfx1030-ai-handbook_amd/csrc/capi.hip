@@ -318,6 +318,51 @@ extern "C" size_t qg_w4a16_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k,
   return 0;
 }
 
+extern "C" int qg_w4a8_gemm(const int8_t* a, int64_t a_sm, int64_t m, int64_t k, const int32_t* w, int64_t n,
+                            int group_size, int flags, const void* scales, int scales_dtype, const void* zeros,
+                            const int8_t* prepared, int64_t prepared_sn, const float* a_scale, const void* bias,
+                            int bias_dtype, void* out, int integer, void* stream) {
+  if (!valid_w4_shape(n, k, group_size, flags)) return hipErrorInvalidValue;
+  if (m < 0 || m > kIntMax || m * n >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  // the integer bound of int4_weight_gemm_v07.py:493 (k * 128 * 15 < 2^31)
+  if (k * 128 * 15 >= (int64_t(1) << 31) || (integer != 0 && integer != 1)) return hipErrorInvalidValue;
+  if (scales_dtype != QG_F32 && scales_dtype != QG_BF16) return hipErrorInvalidValue;
+  if (bias && !float_dtype(bias_dtype)) return hipErrorInvalidValue;
+  // activation rows are copied as 16-byte chunks
+  if (a_sm < k || a_sm % 16 != 0) return hipErrorInvalidValue;
+  if (prepared && (prepared_sn < k || prepared_sn % 16 != 0)) return hipErrorInvalidValue;
+  if (m == 0) return hipSuccess;
+  if (!a || !aligned16(a) || !out || (!integer && !a_scale)) return hipErrorInvalidValue;
+  if (prepared ? (!aligned16(prepared) || (n - 1) * prepared_sn + k >= kMaxOperandBytes)
+               : (!w || !zeros || !aligned16(w)))
+    return hipErrorInvalidValue;
+  if (!integer && !scales) return hipErrorInvalidValue;
+  // activation addresses are 32-bit byte offsets from the base
+  if ((m - 1) * a_sm + k >= kMaxOperandBytes) return hipErrorInvalidValue;
+  qg::W4A8Args p{};
+  p.a = a;
+  p.a_sm = a_sm;
+  p.M = static_cast<int>(m);
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(k);
+  p.w = reinterpret_cast<const uint32_t*>(w);
+  p.w8 = prepared;
+  p.w8_sn = prepared_sn;
+  p.flags = flags;
+  p.group = group_size;
+  p.ng = static_cast<int>(k / group_size);
+  p.zw = (p.ng + 7) / 8;
+  p.scales = scales;
+  p.scale_f32 = scales_dtype == QG_F32;
+  p.zeros = zeros;
+  p.a_scale = a_scale;
+  p.bias = bias;
+  p.bias_dtype = bias_dtype;
+  p.out = out;
+  p.integer = integer;
+  return qg::launch_w4a8_gemm(p, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m, int64_t k,
                              const int32_t* w, int64_t n, int group_size, int flags,
                              const void* scales, int scales_dtype, const void* zeros,

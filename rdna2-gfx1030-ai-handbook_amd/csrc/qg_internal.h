@@ -94,6 +94,29 @@ struct W4Args {
   int out_dtype;
 };
 
+// W4A8 GEMM operands (int4_linear_a8; see include/qgemm.h, qg_w4a8_gemm).
+struct W4A8Args {
+  const int8_t* a;       // activations int8 [M, K], row stride a_sm bytes
+  int64_t a_sm;
+  int M, N, K;
+  const uint32_t* w;     // packed words ([N, K/8] or [K/8, N] per flags), or
+  const int8_t* w8;      // prepared centred int8 weights [N, K] (row stride w8_sn)
+  int64_t w8_sn;
+  int flags;             // qg_w4_flags
+  int group;             // 32, 64 or 128
+  int ng;                // K / group
+  int zw;                // packed zero-point words per row, ceil(ng / 8)
+  const void* scales;    // [N, K/G] fp32 or bf16
+  int scale_f32;
+  const void* zeros;     // int32 [N, K/G] or packed uint4 [N, ceil(K/G/8)]
+  const float* a_scale;  // [M] (float output)
+  const void* bias;      // nullptr or [N] of bias_dtype
+  int bias_dtype;
+  void* out;             // int32 (integer) or fp32 [M, N] contiguous
+  int integer;
+};
+hipError_t launch_w4a8_gemm(const W4A8Args& p, hipStream_t stream);
+
 struct W4PackArgs {
   const void* w;         // [N, K] fp32 / fp16 / bf16, strides in elements
   int w_dtype;

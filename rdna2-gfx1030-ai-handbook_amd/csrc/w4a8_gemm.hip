@@ -1,0 +1,372 @@
+// W4A8 GEMM on gfx950 int8 MFMA: int4_linear_a8 of
+// rdna2-ops/rdna2_ops/int4_weight_gemm_v07.py:476-537. Every method of the
+// reference computes the same numbers (_linear_dot4 :181-217,
+// _linear_dot4_split :220-256, _linear_dot4_words :288-322, _linear_dot8
+// :325-353); they differ only in how the integer group sums are formed:
+//
+//   integer: out[m, n] = sum_g sum_{k in g} a[m, k] (q[n, k] - z[n, g])   int32
+//   float:   total = 0; for g ascending: total = total + f32(acc_g) * s[n, g]
+//            (two fp32 roundings, no FMA: enable_fp_fusion=False)
+//            out = total * sa[m]; out = out + f32(bias[n])                  fp32
+//
+// acc_g is exact (|acc_g| <= 128 * 15 * 128 < 2^24, so f32(acc_g) is exact too).
+//
+// Design (not a translation of the reference's dot4 / dot8 Triton tiles):
+//  * one 128 x 128 output tile per workgroup of 4 waves; wave w owns output
+//    columns 32 w .. 32 w + 31 for all 128 rows: four 32x32 int32 blocks of
+//    v_mfma_i32_32x32x32_i8 with the weight fragment as the first operand, so
+//    a lane holds row 32 i + (l & 31) and 4 adjacent columns per register
+//    quad (columns 8 (r >> 2) + 4 (l >> 5) + (r & 3));
+//  * A stages (128 rows x 128 K bytes) are copied HBM -> LDS with
+//    global_load_lds_dwordx4 into a 2-slot ring in the INT8 GEMM's layout
+//    (128-byte rows, 16-byte chunks XOR-swizzled by (row >> 1) & 7); each lane
+//    loads the packed words of its own weight row for the next stage into
+//    registers (no weight byte is shared between waves), and its zero points;
+//  * a word of 8 nibbles becomes two dwords of bytes u + (16 - zu), with u and
+//    zu the unsigned nibble and zero point: every byte is in [1, 31], so the
+//    zero point costs one 32-bit add and no byte borrows into the next; the
+//    bytes come out in the order (k0 k2 k4 k6)(k1 k3 k5 k7) (the reverse for
+//    the high nibble order) and the A fragment's bytes are permuted to the
+//    same order (4 v_perm_b32 per 16-byte fragment). The MFMA then sums
+//    a (q - z) + 16 a; 16 sum(a) over the group, taken with v_dot4 on the A
+//    fragments, is subtracted when the group ends;
+//  * when a group ends its exact int32 sum is folded into the fp32 total in
+//    the reference's order (the stage's scales are staged in LDS as
+//    [group][column] and read as 4-column vectors) or into an int32 total;
+//  * prepared centred int8 weights (method dot4_prepared) are loaded as 16
+//    bytes per lane and k-step and need neither expansion nor correction.
+#include "qg_common.h"
+#include "qg_internal.h"
+
+namespace qg {
+
+namespace {
+
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kBM = 128, kBN = 128, kThreads = 256;
+constexpr int kStage = 128;                       // K bytes per stage
+constexpr int kSlotA = kBM * kStage;              // 16 KB per A slot
+constexpr int kSlotS = 4 * kBN * 4;               // <= 4 groups x 128 fp32 scales
+constexpr int kLds = 2 * kSlotA + 2 * kSlotS;     // 36 KB
+
+// Output tile of this workgroup (same XCD-aware, GROUP_M-ordered walk as the
+// INT8 GEMM).
+__device__ __forceinline__ void w4a8_tile(int M, int N, int& m0, int& n0) {
+  const int nbm = ceil_div(M, kBM), nbn = ceil_div(N, kBN);
+  const int total = nbm * nbn;
+  int bid = blockIdx.x;
+  if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 4;
+  const int group = bid / (GROUP_M * nbn);
+  const int first = group * GROUP_M;
+  const int gm = min(nbm - first, GROUP_M);
+  const int in_group = bid - group * GROUP_M * nbn;
+  m0 = (first + in_group % gm) * kBM;
+  n0 = (in_group / gm) * kBN;
+}
+
+// Fragment offset in an A slot: k-step t, lane l reads row (l & 31) of a
+// 32-row block, logical chunk 2t + (l >> 5), stored at chunk ^ ((l >> 1) & 7).
+__device__ __forceinline__ int a_frag_offset(int t, int lane) {
+  return (lane & 31) * kStage + (((2 * t + (lane >> 5)) ^ ((lane >> 1) & 7)) << 4);
+}
+
+// Weight registers of one stage: 4 k-steps of a lane's 16 K bytes (2 packed
+// words, or 16 prepared bytes), and the stage's per-group zero-point addends
+// (16 - zu) replicated into the 4 bytes of a dword.
+template <bool PREP>
+struct WStage {
+  uint32_t w[4][PREP ? 4 : 2];
+  uint32_t cb[4];
+};
+
+template <int G, bool PREP, bool INTEGER>
+__global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
+#pragma clang fp contract(off)
+  constexpr int GK = G / 32;      // k-steps per group
+  constexpr int GS = kStage / G;  // groups per stage
+  __shared__ __attribute__((aligned(1024))) char smem[kLds];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, lr = lane & 31;
+  int m0, n0;
+  w4a8_tile(p.M, p.N, m0, n0);
+  const int KT = p.K / 32;                 // k-steps
+  const int S = ceil_div(p.K, kStage);     // stages
+  const uint32_t smem_base = lds_addr_of(smem);
+
+  // ---- A copies: copy I of this wave covers tile rows 8 (wave + 4 I) .. + 7;
+  // lane l fetches logical chunk (l & 7) ^ ((row >> 1) & 7) of its row, rows
+  // clamped into A, and in a last partial stage chunks past K fetch chunk 0
+  // (their LDS bytes are never read).
+  const uint32_t chunk = static_cast<uint32_t>(((lane & 7) ^ (4 * (wave & 1) + (lane >> 4))) << 4);
+  const uint32_t klast = static_cast<uint32_t>(p.K - (S - 1) * kStage);
+  uint32_t aoff[4];
+  for (int i = 0; i < 4; ++i)
+    aoff[i] = static_cast<uint32_t>(min(m0 + wave * 8 + (lane >> 3) + 32 * i, p.M - 1)) *
+              static_cast<uint32_t>(p.a_sm);
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  auto copy_a = [&](int s, int slot) __attribute__((always_inline)) {
+    const uint32_t ch = (s == S - 1 && chunk >= klast) ? 0u : chunk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16s(a_base + static_cast<int64_t>(s) * kStage, aoff[i] + ch,
+             smem_base + slot * kSlotA + (wave + 4 * i) * 1024);
+  };
+
+  // ---- this lane's weight row (output column n0 + 32 wave + (l & 31))
+  const int nw = min(n0 + 32 * wave + lr, p.N - 1);
+  const bool kn = p.flags & QG_W4_LAYOUT_KN;
+  const bool sgn = p.flags & QG_W4_SIGNED_NIBBLES;
+  const bool zpk = p.flags & QG_W4_ZEROS_PACKED;
+  const bool high = p.flags & QG_W4_ORDER_HIGH;
+  // packed word (K index 8 j .. 8 j + 7) of this row: base + j * kstride
+  const uint32_t* wrow = p.w + (kn ? static_cast<int64_t>(nw) : static_cast<int64_t>(nw) * (p.K / 8));
+  const int64_t kstride = kn ? p.N : 1;
+  const uint32_t xmask = sgn ? 0x88888888u : 0u;  // signed nibble q & 15 -> q + 8
+  // A byte permutation matching the nibble extraction order
+  const uint32_t sel0 = high ? 0x01030507u : 0x06040200u;
+  const uint32_t sel1 = high ? 0x00020406u : 0x07050301u;
+
+  auto load_w = [&](int s, WStage<PREP>& b) __attribute__((always_inline)) {
+    static_for<0, 4>([&](auto t_c) {
+      constexpr int t = decltype(t_c)::value;
+      const int kt = min(s * 4 + t, KT - 1);  // k-steps past K load valid, unused data
+      if constexpr (PREP) {
+        const i32x4 v = *reinterpret_cast<const i32x4*>(p.w8 + static_cast<int64_t>(nw) * p.w8_sn + kt * 32 + 16 * h);
+        static_for<0, 4>([&](auto e) { b.w[t][e] = static_cast<uint32_t>(v[decltype(e)::value]); });
+      } else {
+        const int64_t j = 4 * kt + 2 * h;
+        b.w[t][0] = wrow[j * kstride];
+        b.w[t][1] = wrow[(j + 1) * kstride];
+      }
+    });
+    if constexpr (!PREP) {
+      static_for<0, GS>([&](auto gi_c) {
+        constexpr int gi = decltype(gi_c)::value;
+        const int g = min(s * GS + gi, p.ng - 1);
+        int zu;
+        if (zpk) {
+          const uint32_t zword = static_cast<const uint32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.zw + (g >> 3)];
+          const int z = static_cast<int>((zword >> (4 * (g & 7))) & 15u);
+          zu = sgn ? (z ^ 8) : z;
+        } else {
+          const int z = static_cast<const int32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.ng + g];
+          zu = sgn ? z + 8 : z;
+        }
+        b.cb[gi] = static_cast<uint32_t>(16 - zu) * 0x01010101u;
+      });
+    }
+  };
+
+  // ---- scales of a stage: thread t covers column t & 127 and the stage's
+  // groups (t >> 7) and (t >> 7) + 2 (clamped; only valid ones are stored)
+  const int scol = tid & (kBN - 1), sg0 = tid >> 7;
+  const int scn = min(n0 + scol, p.N - 1);
+  auto load_scales = [&](int s, float (&sc)[2]) __attribute__((always_inline)) {
+    if constexpr (!INTEGER) {
+      static_for<0, 2>([&](auto j_c) {
+        constexpr int j = decltype(j_c)::value;
+        const int gi = min(sg0 + 2 * j, GS - 1);
+        const int g = min(s * GS + gi, p.ng - 1);
+        const int64_t i = static_cast<int64_t>(scn) * p.ng + g;
+        sc[j] = p.scale_f32 ? static_cast<const float*>(p.scales)[i]
+                            : bf16_to_f32(static_cast<const uint16_t*>(p.scales)[i]);
+      });
+    }
+  };
+  auto park_scales = [&](int slot, const float (&sc)[2]) __attribute__((always_inline)) {
+    if constexpr (!INTEGER) {
+      float* dst = reinterpret_cast<float*>(smem + 2 * kSlotA + slot * kSlotS);
+      static_for<0, 2>([&](auto j_c) {
+        constexpr int j = decltype(j_c)::value;
+        const int gi = sg0 + 2 * j;
+        if (gi < GS) dst[gi * kBN + scol] = sc[j];
+      });
+    }
+  };
+
+  i32x16 acc[4];
+  float tot[4][16];
+  int itot[4][16];
+  int asum[4];
+  static_for<0, 4>([&](auto i) {
+    asum[i] = 0;
+    static_for<0, 16>([&](auto r) {
+      tot[i][r] = 0.0f;
+      itot[i][r] = 0;
+    });
+  });
+
+  // Fold the finished group gi of the stage in slot `slot` into the totals.
+  auto flush = [&](int slot, int gi) __attribute__((always_inline)) {
+    const float* scl = reinterpret_cast<const float*>(smem + 2 * kSlotA + slot * kSlotS) + gi * kBN;
+    static_for<0, 4>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      int corr = 0;
+      if constexpr (!PREP) {
+        corr = 16 * (asum[i] + __shfl_xor(asum[i], 32, 64));
+        asum[i] = 0;
+      }
+      static_for<0, 4>([&](auto q_c) {
+        constexpr int q = decltype(q_c)::value;
+        f32x4 s4 = {0, 0, 0, 0};
+        if constexpr (!INTEGER) s4 = *reinterpret_cast<const f32x4*>(scl + 32 * wave + 8 * q + 4 * h);
+        static_for<0, 4>([&](auto c_c) {
+          constexpr int c = decltype(c_c)::value;
+          const int v = acc[i][4 * q + c] - corr;
+          if constexpr (INTEGER) itot[i][4 * q + c] += v;
+          else tot[i][4 * q + c] = tot[i][4 * q + c] + static_cast<float>(v) * s4[c];
+        });
+      });
+    });
+  };
+
+  // MFMAs of stage s (A in slot s & 1, weights in b).
+  auto compute = [&](int s, const WStage<PREP>& b) __attribute__((always_inline)) {
+    const int slot = s & 1;
+    const char* abase = smem + slot * kSlotA;
+    static_for<0, 4>([&](auto t_c) {
+      constexpr int t = decltype(t_c)::value;
+      if (s * 4 + t < KT) {
+        i32x4 af[4];
+        static_for<0, 4>([&](auto i_c) {
+          constexpr int i = decltype(i_c)::value;
+          const i32x4 raw = *reinterpret_cast<const i32x4*>(abase + i * 32 * kStage + a_frag_offset(t, lane));
+          if constexpr (PREP) {
+            af[i] = raw;
+          } else {
+            int sm = asum[i];
+            static_for<0, 4>([&](auto e) { sm = __builtin_amdgcn_sdot4(raw[decltype(e)::value], 0x01010101, sm, false); });
+            asum[i] = sm;
+            const uint32_t d0 = raw[0], d1 = raw[1], d2 = raw[2], d3 = raw[3];
+            af[i] = i32x4{static_cast<int>(__builtin_amdgcn_perm(d1, d0, sel0)),
+                          static_cast<int>(__builtin_amdgcn_perm(d1, d0, sel1)),
+                          static_cast<int>(__builtin_amdgcn_perm(d3, d2, sel0)),
+                          static_cast<int>(__builtin_amdgcn_perm(d3, d2, sel1))};
+          }
+        });
+        i32x4 wf;
+        if constexpr (PREP) {
+          wf = i32x4{static_cast<int>(b.w[t][0]), static_cast<int>(b.w[t][1]), static_cast<int>(b.w[t][2]),
+                     static_cast<int>(b.w[t][3])};
+        } else {
+          const uint32_t c = b.cb[t / GK];
+          const uint32_t x0 = b.w[t][0] ^ xmask, x1 = b.w[t][1] ^ xmask;
+          wf = i32x4{static_cast<int>((x0 & 0x0F0F0F0Fu) + c), static_cast<int>(((x0 >> 4) & 0x0F0F0F0Fu) + c),
+                     static_cast<int>((x1 & 0x0F0F0F0Fu) + c), static_cast<int>(((x1 >> 4) & 0x0F0F0F0Fu) + c)};
+        }
+        static_for<0, 4>([&](auto i_c) {
+          constexpr int i = decltype(i_c)::value;
+          if constexpr (t % GK == 0) acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, af[i], i32x16{}, 0, 0, 0);
+          else acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, af[i], acc[i], 0, 0, 0);
+        });
+        if constexpr ((t + 1) % GK == 0) flush(slot, t / GK);
+      }
+    });
+  };
+
+  // ---- pipeline: stage s + 1's copies and loads are issued before stage s
+  // computes; one barrier per stage.
+  WStage<PREP> wb[2];
+  float sc[2] = {0.0f, 0.0f};
+  copy_a(0, 0);
+  load_w(0, wb[0]);
+  load_scales(0, sc);
+  wait_vm<0>();
+  park_scales(0, sc);
+  wait_lds_barrier();
+  auto stage = [&](int s, auto cur_c) __attribute__((always_inline)) {
+    constexpr int cur = decltype(cur_c)::value;
+    if (s + 1 < S) {
+      copy_a(s + 1, (s + 1) & 1);
+      load_w(s + 1, wb[cur ^ 1]);
+      load_scales(s + 1, sc);
+    }
+    compute(s, wb[cur]);
+    if (s + 1 < S) {
+      wait_vm<0>();
+      park_scales((s + 1) & 1, sc);
+    }
+    wait_vm_barrier<0>();  // stage s + 1 landed everywhere; slot s & 1 free
+  };
+  int s = 0;
+  for (; s + 1 < S; s += 2) {
+    stage(s, std::integral_constant<int, 0>{});
+    stage(s + 1, std::integral_constant<int, 1>{});
+  }
+  if (s < S) stage(s, std::integral_constant<int, 0>{});
+
+  // ---- output: row m0 + 32 i + (l & 31), columns n0 + 32 wave + 8 q + 4 h + c
+  const bool vec = (p.N % 4) == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+  static_for<0, 4>([&](auto i_c) {
+    constexpr int i = decltype(i_c)::value;
+    const int row = m0 + 32 * i + lr;
+    if (row >= p.M) return;
+    float sa = 0.0f;
+    if constexpr (!INTEGER) sa = p.a_scale[row];
+    static_for<0, 4>([&](auto q_c) {
+      constexpr int q = decltype(q_c)::value;
+      const int col0 = n0 + 32 * wave + 8 * q + 4 * h;
+      uint32_t bits[4];
+      static_for<0, 4>([&](auto c_c) {
+        constexpr int c = decltype(c_c)::value;
+        if constexpr (INTEGER) {
+          bits[c] = static_cast<uint32_t>(itot[i][4 * q + c]);
+        } else {
+          float y = tot[i][4 * q + c] * sa;
+          if (p.bias != nullptr) {
+            const int col = min(col0 + c, p.N - 1);
+            float bv;
+            if (p.bias_dtype == QG_F32) bv = static_cast<const float*>(p.bias)[col];
+            else if (p.bias_dtype == QG_F16) bv = f16_to_f32(static_cast<const uint16_t*>(p.bias)[col]);
+            else bv = bf16_to_f32(static_cast<const uint16_t*>(p.bias)[col]);
+            y = y + bv;
+          }
+          bits[c] = __float_as_uint(y);
+        }
+      });
+      uint32_t* orow = static_cast<uint32_t*>(p.out) + static_cast<int64_t>(row) * p.N;
+      if (vec && col0 + 4 <= p.N) {
+        *reinterpret_cast<i32x4*>(orow + col0) =
+            i32x4{static_cast<int>(bits[0]), static_cast<int>(bits[1]), static_cast<int>(bits[2]),
+                  static_cast<int>(bits[3])};
+      } else {
+        static_for<0, 4>([&](auto c_c) {
+          constexpr int c = decltype(c_c)::value;
+          if (col0 + c < p.N) orow[col0 + c] = bits[c];
+        });
+      }
+    });
+  });
+}
+
+template <int G, bool PREP>
+hipError_t launch_g(const W4A8Args& p, hipStream_t stream) {
+  const int blocks = ceil_div(p.M, kBM) * ceil_div(p.N, kBN);
+  if (p.integer)
+    hipLaunchKernelGGL((k_w4a8<G, PREP, true>), dim3(blocks), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((k_w4a8<G, PREP, false>), dim3(blocks), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <bool PREP>
+hipError_t launch_p(const W4A8Args& p, hipStream_t stream) {
+  if (p.group == 32) return launch_g<32, PREP>(p, stream);
+  if (p.group == 64) return launch_g<64, PREP>(p, stream);
+  return launch_g<128, PREP>(p, stream);
+}
+
+}  // namespace
+
+hipError_t launch_w4a8_gemm(const W4A8Args& p, hipStream_t stream) {
+  if (p.M == 0 || p.N == 0) return hipSuccess;
+  return p.w8 != nullptr ? launch_p<true>(p, stream) : launch_p<false>(p, stream);
+}
+
+}  // namespace qg

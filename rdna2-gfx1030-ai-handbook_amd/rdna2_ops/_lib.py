@@ -63,6 +63,8 @@ SIGNATURES = {
     "qg_w4a16_gemm_workspace_bytes": (_sz, [_i64, _i64, _i64, _i, _i]),
     "qg_w4a16_gemm": (_i, [_p, _i, _i64, _i64, _i64, _p, _i64, _i, _i, _p, _i, _p, _p, _i, _p, _i,
                            _p, _sz, _p]),
+    "qg_w4a8_gemm": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i, _i, _p, _i, _p, _p, _i64, _p, _p, _i, _p, _i,
+                          _p]),
     "qg_fp8_decode": (_i, [_p, _i, _i64, _i64, _i64, _i64, _p, _i, _p]),
     "qg_fp8w_gemm_workspace_bytes": (_sz, [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64]),
     "qg_fp8w_gemm": (_i, [_p, _i, _i64, _i64, _i64, _i64, _p, _i, _i64, _i64, _i64, _p, _p, _i, _p, _i,

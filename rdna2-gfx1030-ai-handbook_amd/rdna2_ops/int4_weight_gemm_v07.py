@@ -18,6 +18,13 @@ device work runs in hand-written gfx950 HIP kernels of librdna2_qgemm.so
             sum in fp32 (the reference's dot2 rounds each weight to fp16 first).
   fused     alias of dot2.
 
+``int4_linear_a8`` (W4A8, int8 activations with a per-row scale): every
+method of the reference (dot4, dot4_prepared, dot4_split, dot4_words, dot8)
+runs one gfx950 kernel on the int8 MFMA with the reference's exact integer
+group sums and fp32 group-scale order (bit-identical results);
+``prepare_dot8_activation`` and ``int8_activation_to_fp16`` keep their
+interfaces.
+
 Extensions (defaults keep the reference's behaviour): bf16 activations (the
 output and bias then are bf16), and the BASELINE configuration-2 storage
 ``pack_uint4`` — unsigned nibbles, bf16 scales, uint4 zero points packed 8 per
@@ -291,4 +298,111 @@ def int4_linear_a16(a, p, *, bias=None, method="dequant", prepared=None, tile=(6
     if return_kernel:
         fm = 1 if a.shape[0] <= 16 else 2 if a.shape[0] <= 32 else 4
         return out, _lib.kernel_metadata("w4a16_skinny", (16 * fm, 16, 128), "k_w4_skinny")
+    return out
+
+
+# ------------------------------------------------------------------ W4A8
+_A8_METHODS = ("dot4", "dot4_prepared", "dot4_split", "dot4_words", "dot8")
+
+
+def prepare_dot8_activation(a, p):
+    """The reference's exact A8 recoding for its dot8 kernel
+    (int4_weight_gemm_v07.py:455-464, _pack_a8 :156-171): caller-owned
+    (low-nibble words of (a & 15) ^ 8, high-nibble words of (a >> 4) & 15,
+    per-group sums of a). Kept for interface compatibility: the gfx950 W4A8
+    kernel multiplies the int8 activations directly, so int4_linear_a8 only
+    validates a prepared tuple and computes from ``a``."""
+    _validate(p)
+    if a.dtype != torch.int8 or a.ndim != 2 or a.shape[1] != p.k or a.device != p.data.device or min(a.stride()) <= 0:
+        raise ValueError("Matching positive-stride A8[M,K] required")
+    m, k = a.shape
+    ai = a.to(torch.int64)
+    shifts = torch.arange(8, device=a.device, dtype=torch.int64) * 4
+    if p.order == "high":
+        shifts = 28 - shifts
+
+    def words(nib):
+        v = (nib.reshape(m, k // 8, 8) << shifts).sum(-1)
+        return (((v + 2 ** 31) % 2 ** 32) - 2 ** 31).to(torch.int32)
+
+    lo = words((ai & 15) ^ 8)
+    hi = words((ai >> 4) & 15)
+    sums = ai.reshape(m, k // p.group_size, p.group_size).sum(-1).to(torch.int32)
+    return lo, hi, sums
+
+
+def int8_activation_to_fp16(a, scale):
+    """fp16 [M, K] = fp32(a) * scale[m] rounded once (int4_weight_gemm_v07.py:467-471)."""
+    m, k = a.shape
+    return (a.to(torch.float32) * scale.reshape(-1, 1).to(torch.float32)).to(torch.float16).reshape(m, k)
+
+
+def int4_linear_a8(a, p, a_scale, *, bias=None, method="dot4", tile=(64, 64), num_warps=4,
+                   prepared=None, integer=False, return_kernel=False):
+    """(A8 * row scale) @ reconstructed W4^T, fp32 output (int32 with
+    ``integer``) — int4_weight_gemm_v07.py:476-537, argument checks in the
+    reference's order.
+
+    Every method computes the same numbers in the reference: per K group the
+    exact integer sum of a * (q - z), folded into an fp32 total as
+    total = total + f32(sum) * scale[n, g] (groups ascending, separate
+    roundings), then * a_scale[m], then + bias. Here all of them run one
+    gfx950 kernel on the int8 MFMA (qg_w4a8_gemm) that produces those bits;
+    dot4_prepared feeds the caller's centred INT8 weights instead of the
+    packed words. ``tile`` / ``num_warps`` are validated, not used."""
+    _validate(p)
+    _eager(a)
+    if (a.ndim != 2 or a.dtype != torch.int8 or a.device != p.data.device or a.shape[1] != p.k
+            or min(a.stride()) <= 0 or a.shape[0] * p.n >= 2 ** 31):
+        raise ValueError("Matching A8[M,K] required")
+    m, k = a.shape
+    if (a_scale.shape not in ((m,), (m, 1)) or a_scale.device != a.device or a_scale.dtype != torch.float32
+            or not a_scale.is_contiguous()):
+        raise ValueError("Contiguous FP32 per-activation-row scale required")
+    if bias is not None and (bias.shape != (p.n,) or bias.device != a.device or not bias.is_contiguous()
+                             or not bias.is_floating_point()):
+        raise ValueError("Floating bias [N] required")
+    if len(tile) != 2 or any(x not in (8, 16, 32, 64, 128) for x in tile) or num_warps not in (4, 8):
+        raise ValueError("Unsupported tile/warps")
+    if k * 128 * 15 >= 2 ** 31:
+        raise ValueError("Integer accumulator bound exceeded")
+    out = torch.empty((m, p.n), device=a.device, dtype=torch.int32 if integer else torch.float32)
+    bm, bn = tile
+    w8 = None
+    if method == "dot8":
+        # the kernel needs no recoding of A; a caller's prepared tuple is checked
+        if prepared is not None:
+            if not isinstance(prepared, tuple) or len(prepared) != 3:
+                raise ValueError("Dot8 prepared tuple required")
+            al, ah, asum = prepared
+            if (any(t.device != a.device or t.dtype != torch.int32 or not t.is_contiguous() for t in prepared)
+                    or al.shape != (m, k // 8) or ah.shape != al.shape or asum.shape != (m, k // p.group_size)):
+                raise ValueError("Invalid prepared activation shape/dtype")
+    elif method in ("dot4", "dot4_prepared"):
+        if method == "dot4_prepared":
+            if prepared is None or prepared.shape != (p.n, k) or prepared.dtype != torch.int8 or prepared.device != a.device:
+                raise ValueError("Centered INT8 prepared weight required")
+            w8 = prepared if prepared.stride(1) == 1 and prepared.stride(0) % 16 == 0 and prepared.data_ptr() % 16 == 0 \
+                else prepared.contiguous()
+        if bm < 16 or bn < 16:
+            raise ValueError("tl.dot tile dimensions must be >=16")
+    elif method == "dot4_split":
+        if bm < 16 or bn < 16:
+            raise ValueError("tl.dot tile dimensions must be >=16")
+    elif method != "dot4_words":
+        raise ValueError(method)
+    if m:
+        # unit-K-stride rows on 16-byte boundaries for the kernel's copies
+        av = a if a.stride(1) == 1 and a.stride(0) % 16 == 0 and a.data_ptr() % 16 == 0 else a.contiguous()
+        b = bias
+        if b is not None and b.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            b = b.to(torch.float32)
+        _lib.check(_lib.library().qg_w4a8_gemm(
+            _lib.ptr(av), av.stride(0), m, k, _lib.ptr(p.data), p.n, p.group_size, p.flags,
+            _lib.ptr(p.scales), _lib.DTYPE_CODE[p.scales.dtype], _lib.ptr(p.zeros), _lib.ptr(w8),
+            w8.stride(0) if w8 is not None else 0, _lib.ptr(a_scale), _lib.ptr(b),
+            _lib.DTYPE_CODE[b.dtype] if b is not None else 0, _lib.ptr(out), int(integer), _lib.stream_of(av)),
+            "qg_w4a8_gemm")
+    if return_kernel:
+        return out, _lib.kernel_metadata("w4a8_mfma_i32_32x32x32_i8", (128, 128), "k_w4a8")
     return out

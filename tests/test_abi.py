@@ -85,3 +85,25 @@ def test_w8a8_linear_rejects_invalid_arguments(lib):
     bad[1] = _lib.I8
     assert lib.qg_w8a8_linear(*bad) == INVALID
     assert lib.qg_w8a8_linear_workspace_bytes(p, 64, 4, 4, 64) >= 4 * 64 + 16
+
+
+def test_w4a8_gemm_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    base = dict(a=p, a_sm=256, m=4, k=256, w=p, n=8, group=32, flags=_lib.W4_SIGNED_NIBBLES, scales=p,
+                scales_dtype=_lib.F32, zeros=p, prepared=None, prepared_sn=0, a_scale=p, bias=None, bias_dtype=0,
+                out=p, integer=0, stream=None)
+
+    def call(**kw):
+        return lib.qg_w4a8_gemm(*dict(base, **kw).values())
+
+    assert call(group=48) == INVALID                       # group size 32 / 64 / 128
+    assert call(k=96, a_sm=96, group=64) == INVALID        # k % group
+    assert call(k=1118496, a_sm=1118496) == INVALID        # k * 128 * 15 >= 2^31 (int4_weight_gemm_v07.py:493)
+    assert call(a_sm=264) == INVALID                       # rows on 16-byte boundaries
+    assert call(a=ctypes.c_void_p(24)) == INVALID          # 16-byte aligned base
+    assert call(a_scale=None) == INVALID                   # float output needs the row scale
+    assert call(scales_dtype=_lib.F16) == INVALID
+    assert call(flags=64) == INVALID
+    assert call(integer=2) == INVALID
+    assert call(prepared=p, prepared_sn=100) == INVALID    # prepared rows on 16-byte boundaries
+    assert call(m=0) == 0                                  # empty output: nothing to launch

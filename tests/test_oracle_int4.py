@@ -155,3 +155,87 @@ def test_pack_rejects_bad_arguments():
     w[0, 0] = np.inf
     with pytest.raises(ValueError):
         o4.pack_int4_ref(w, group_size=32)
+
+
+# ----------------------------------------------------------------- W4A8
+def _a8_case(seed, m, n, k, g, sym=False):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-128, 128, (m, k)).astype(np.int8)
+    w = (rng.standard_normal((n, k)) * 0.01).astype(np.float32)
+    p = o4.pack_int4_ref(w, group_size=g, symmetric=sym)
+    centred = o4.unpack_int4_ref(p, floating=False)
+    sa = (rng.random(m) * 0.02 + 0.001).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.01).astype(np.float32)
+    return a, centred, p["scales"], sa, bias
+
+
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_w4a8_oracle_matches_scalar_loops(g):
+    """The vectorised oracle equals scalar loops with one float32 rounding per
+    operation, bit for bit (float and integer results)."""
+    a, c, s, sa, bias = _a8_case(g, 3, 5, 2 * g, g)
+    assert np.array_equal(o4.w4a8_linear(a, c, s, sa, g, bias), o4.w4a8_linear_bruteforce(a, c, s, sa, g, bias))
+    assert np.array_equal(o4.w4a8_linear(a, c, s, sa, g), o4.w4a8_linear_bruteforce(a, c, s, sa, g))
+    ref = np.array([[sum(int(a[i, kk]) * int(c[j, kk]) for kk in range(a.shape[1])) for j in range(5)]
+                    for i in range(3)])
+    assert np.array_equal(o4.w4a8_integer(a, c), ref)
+
+
+def test_w4a8_oracle_matches_torch_grouped_reference():
+    """The reference's own grouped reference (int4_model_switches_v07.py:19-34:
+    torch fp32 mm per group, which is exact here, then torch mul / add in
+    the declared order), formulated with torch on the CPU, is bit-identical."""
+    import torch
+    a, c, s, sa, bias = _a8_case(7, 37, 53, 384, 32)
+    at, ct = torch.from_numpy(a), torch.from_numpy(c.astype(np.int8))
+    st = torch.from_numpy(s)
+    total = torch.zeros((37, 53), dtype=torch.float32)
+    for gi in range(384 // 32):
+        exact = torch.mm(at[:, gi * 32:(gi + 1) * 32].float(), ct[:, gi * 32:(gi + 1) * 32].float().T)
+        total = total + exact * st[:, gi][None, :]
+    y = total * torch.from_numpy(sa).reshape(-1, 1) + torch.from_numpy(bias).reshape(1, -1)
+    assert np.array_equal(o4.w4a8_linear(a, c, s, sa, 32, bias), y.numpy())
+
+
+def test_w4a8_closed_forms():
+    """Unit scales and no bias: the float result is the exact integer product
+    (|sum| < 2^24); a = 1 everywhere: column sums of q - z."""
+    a, c, s, sa, _ = _a8_case(3, 6, 7, 256, 64)
+    ones_s = np.ones_like(s)
+    ones_a = np.ones(6, np.float32)
+    assert np.array_equal(o4.w4a8_linear(a, c, ones_s, ones_a, 64), o4.w4a8_integer(a, c).astype(np.float32))
+    a1 = np.ones((2, 256), np.int8)
+    assert np.array_equal(o4.w4a8_integer(a1, c), np.repeat(c.sum(1)[None, :], 2, 0))
+
+
+def test_w4a8_planted_mistakes_are_caught():
+    """Plausible slips — the zero point dropped, the row scale applied per
+    group before the sum, the groups summed in reverse, one fused multiply-add
+    instead of two roundings — each change the result."""
+    a, c, s, sa, bias = _a8_case(11, 16, 24, 512, 32)
+    good = o4.w4a8_linear(a, c, s, sa, 32, bias)
+    # zero point dropped: q instead of q - z
+    p = o4.pack_int4_ref((np.random.default_rng(11).standard_normal((24, 512)) * 0.01).astype(np.float32),
+                         group_size=32, symmetric=False)
+    assert (p["zeros"] != 0).any()
+    c2 = o4.unpack_int4_ref(p, floating=False)
+    q = c2 + np.repeat(p["zeros"], 32, axis=1)
+    assert not np.array_equal(o4.w4a8_linear(a, q, p["scales"], sa, 32, bias),
+                              o4.w4a8_linear(a, c2, p["scales"], sa, 32, bias))
+    # row scale inside the group loop
+    a64, c64 = a.astype(np.float64), c.astype(np.float64)
+    t1 = np.zeros((16, 24), np.float32)
+    t2 = np.zeros((16, 24), np.float32)
+    t3 = np.zeros((16, 24), np.float32)
+    for gi in range(16):
+        sl = slice(gi * 32, gi * 32 + 32)
+        acc = (a64[:, sl] @ c64[:, sl].T).astype(np.float32)
+        t1 = (t1 + ((acc * s[:, gi][None, :]).astype(np.float32) * sa[:, None]).astype(np.float32)).astype(np.float32)
+        t3 = (acc.astype(np.float64) * s[:, gi][None, :].astype(np.float64) + t3.astype(np.float64)).astype(np.float32)
+    for gi in reversed(range(16)):
+        sl = slice(gi * 32, gi * 32 + 32)
+        acc = (a64[:, sl] @ c64[:, sl].T).astype(np.float32)
+        t2 = (t2 + (acc * s[:, gi][None, :]).astype(np.float32)).astype(np.float32)
+    assert not np.array_equal((t1 + bias[None, :]).astype(np.float32), good)
+    assert not np.array_equal(((t2 * sa[:, None]).astype(np.float32) + bias[None, :]).astype(np.float32), good)
+    assert not np.array_equal(((t3 * sa[:, None]).astype(np.float32) + bias[None, :]).astype(np.float32), good)

@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=("w4a16", "fp8", "moe"), default=None,
+    ap.add_argument("--only", choices=("w4a16", "fp8", "moe", "w4a8"), default=None,
                     help="run one secondary measurement alone and print it (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -260,6 +260,37 @@ def run_moe(torch, dev, iters=20):
             "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "ops": ops, "bytes": nbytes}
 
 
+def run_w4a8(torch, dev, iters=20):
+    """Secondary (SURVEY next row, no BASELINE config): W4A8 on the int8 MFMA,
+    int4_linear_a8 float output, on the cfg0 shape with g128 affine nk
+    weights and on the reference's own check shape (M 1061, g32, kn).
+    TOPS = 2 M N K per call; HIP events over `iters` back-to-back calls."""
+    from rdna2_ops import int4_weight_gemm_v07 as w4
+    res = {}
+    for label, (m, n, k, g, layout) in (("cfg0_shape_g128", (4096, 3072, 3072, 128, "nk")),
+                                        ("moss_1061_g32_kn", (1061, 3072, 3072, 32, "kn"))):
+        gen = torch.Generator(device=dev).manual_seed(7)
+        w = torch.randn(n, k, device=dev, generator=gen) * 0.01
+        p = w4.pack_int4(w, group_size=g, symmetric=False, layout=layout)
+        a = torch.randint(-128, 128, (m, k), dtype=torch.int8, device=dev, generator=gen)
+        sa = torch.rand(m, device=dev, generator=gen) * 0.01
+        for _ in range(3):
+            w4.int4_linear_a8(a, p, sa)
+        torch.cuda.synchronize()
+        s = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(iters):
+            w4.int4_linear_a8(a, p, sa)
+        e1.record(s)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) / iters * 1e3
+        tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+        res[label] = {"us": round(us, 1), "TOPS": round(tops, 1), "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4),
+                      "shape": [m, n, k], "group": g}
+    return res
+
+
 def traffic_bytes(name="int8_gemm_cfg1_chain_traffic.json"):
     """HBM bytes per launch of a kernel, measured with rocprofv3 --pmc
     FETCH_SIZE / WRITE_SIZE (scaled by a plain-copy calibration) and recorded in
@@ -296,7 +327,7 @@ def main():
     lib = _lib.library()
     if args.only:
         runs = {"w4a16": lambda: run_w4a16(torch, lib, _lib, dev), "fp8": lambda: run_fp8(torch, lib, _lib, dev),
-                "moe": lambda: run_moe(torch, dev)}
+                "moe": lambda: run_moe(torch, dev), "w4a8": lambda: run_w4a8(torch, dev)}
         res = runs[args.only]()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return
@@ -360,6 +391,7 @@ def main():
         sec["w4a16_prefill_m2048"] = w4[2048]
         sec["fp8_cfg3"] = run_fp8(torch, lib, _lib, dev)
         sec["moe_cfg4"] = run_moe(torch, dev)
+        sec["w4a8"] = run_w4a8(torch, dev)
         line["secondary"] = sec
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import time_cfg1_chain

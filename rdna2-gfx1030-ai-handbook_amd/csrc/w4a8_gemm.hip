@@ -22,19 +22,17 @@
 //    (128-byte rows, 16-byte chunks XOR-swizzled by (row >> 1) & 7); each lane
 //    loads the packed words of its own weight row for the next stage into
 //    registers (no weight byte is shared between waves), and its zero points;
-//  * a word of 8 nibbles becomes two dwords of bytes u + (16 - zu), with u and
-//    zu the unsigned nibble and zero point: every byte is in [1, 31], so the
-//    zero point costs one 32-bit add and no byte borrows into the next; the
-//    bytes come out in the order (k0 k2 k4 k6)(k1 k3 k5 k7) (the reverse for
-//    the high nibble order) and the A fragment's bytes are permuted to the
-//    same order (4 v_perm_b32 per 16-byte fragment). The MFMA then sums
-//    a (q - z) + 16 a; 16 sum(a) over the group, taken with v_dot4 on the A
-//    fragments, is subtracted when the group ends;
+//  * a word of 8 nibbles becomes two dwords of signed bytes q - z without any
+//    borrow between bytes: with u, zu the unsigned nibble and zero point,
+//    ((u | 0x80) - zu) ^ 0x80 per byte (128 + u - zu never goes below 113, and
+//    flipping bit 7 turns the excess-128 value into two's complement), then
+//    two v_perm_b32 interleave the even and odd nibbles back into K order.
+//    The MFMA sums a (q - z) exactly, against the A fragment as it lies in LDS;
 //  * when a group ends its exact int32 sum is folded into the fp32 total in
 //    the reference's order (the stage's scales are staged in LDS as
 //    [group][column] and read as 4-column vectors) or into an int32 total;
 //  * prepared centred int8 weights (method dot4_prepared) are loaded as 16
-//    bytes per lane and k-step and need neither expansion nor correction.
+//    bytes per lane and k-step and need no expansion.
 #include "qg_common.h"
 #include "qg_internal.h"
 
@@ -74,12 +72,12 @@ __device__ __forceinline__ int a_frag_offset(int t, int lane) {
 }
 
 // Weight registers of one stage: 4 k-steps of a lane's 16 K bytes (2 packed
-// words, or 16 prepared bytes), and the stage's per-group zero-point addends
-// (16 - zu) replicated into the 4 bytes of a dword.
+// words, or 16 prepared bytes), and the stage's per-group unsigned zero points
+// replicated into the 4 bytes of a dword.
 template <bool PREP>
 struct WStage {
   uint32_t w[4][PREP ? 4 : 2];
-  uint32_t cb[4];
+  uint32_t zb[4];
 };
 
 template <int G, bool PREP, bool INTEGER>
@@ -128,9 +126,12 @@ __global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
   const uint32_t* wrow = p.w + (kn ? static_cast<int64_t>(nw) : static_cast<int64_t>(nw) * (p.K / 8));
   const int64_t kstride = kn ? p.N : 1;
   const uint32_t xmask = sgn ? 0x88888888u : 0u;  // signed nibble q & 15 -> q + 8
-  // A byte permutation matching the nibble extraction order
-  const uint32_t sel0 = high ? 0x01030507u : 0x06040200u;
-  const uint32_t sel1 = high ? 0x00020406u : 0x07050301u;
+  // K order from the even-nibble bytes (lo) and odd-nibble bytes (hi):
+  // low order lo = (k0 k2 k4 k6), hi = (k1 k3 k5 k7); high order lo =
+  // (k7 k5 k3 k1), hi = (k6 k4 k2 k0); v_perm_b32(hi, lo, sel) picks bytes
+  // 0-3 of lo and 4-7 of hi
+  const uint32_t sel0 = high ? 0x02060307u : 0x05010400u;  // k0 k1 k2 k3
+  const uint32_t sel1 = high ? 0x00040105u : 0x07030602u;  // k4 k5 k6 k7
 
   auto load_w = [&](int s, WStage<PREP>& b) __attribute__((always_inline)) {
     static_for<0, 4>([&](auto t_c) {
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
           const int z = static_cast<const int32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.ng + g];
           zu = sgn ? z + 8 : z;
         }
-        b.cb[gi] = static_cast<uint32_t>(16 - zu) * 0x01010101u;
+        b.zb[gi] = static_cast<uint32_t>(zu) * 0x01010101u;
       });
     }
   };
@@ -193,9 +194,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
   i32x16 acc[4];
   float tot[4][16];
   int itot[4][16];
-  int asum[4];
   static_for<0, 4>([&](auto i) {
-    asum[i] = 0;
     static_for<0, 16>([&](auto r) {
       tot[i][r] = 0.0f;
       itot[i][r] = 0;
@@ -207,18 +206,13 @@ __global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
     const float* scl = reinterpret_cast<const float*>(smem + 2 * kSlotA + slot * kSlotS) + gi * kBN;
     static_for<0, 4>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
-      int corr = 0;
-      if constexpr (!PREP) {
-        corr = 16 * (asum[i] + __shfl_xor(asum[i], 32, 64));
-        asum[i] = 0;
-      }
       static_for<0, 4>([&](auto q_c) {
         constexpr int q = decltype(q_c)::value;
         f32x4 s4 = {0, 0, 0, 0};
         if constexpr (!INTEGER) s4 = *reinterpret_cast<const f32x4*>(scl + 32 * wave + 8 * q + 4 * h);
         static_for<0, 4>([&](auto c_c) {
           constexpr int c = decltype(c_c)::value;
-          const int v = acc[i][4 * q + c] - corr;
+          const int v = acc[i][4 * q + c];
           if constexpr (INTEGER) itot[i][4 * q + c] += v;
           else tot[i][4 * q + c] = tot[i][4 * q + c] + static_cast<float>(v) * s4[c];
         });
@@ -236,29 +230,25 @@ __global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
         i32x4 af[4];
         static_for<0, 4>([&](auto i_c) {
           constexpr int i = decltype(i_c)::value;
-          const i32x4 raw = *reinterpret_cast<const i32x4*>(abase + i * 32 * kStage + a_frag_offset(t, lane));
-          if constexpr (PREP) {
-            af[i] = raw;
-          } else {
-            int sm = asum[i];
-            static_for<0, 4>([&](auto e) { sm = __builtin_amdgcn_sdot4(raw[decltype(e)::value], 0x01010101, sm, false); });
-            asum[i] = sm;
-            const uint32_t d0 = raw[0], d1 = raw[1], d2 = raw[2], d3 = raw[3];
-            af[i] = i32x4{static_cast<int>(__builtin_amdgcn_perm(d1, d0, sel0)),
-                          static_cast<int>(__builtin_amdgcn_perm(d1, d0, sel1)),
-                          static_cast<int>(__builtin_amdgcn_perm(d3, d2, sel0)),
-                          static_cast<int>(__builtin_amdgcn_perm(d3, d2, sel1))};
-          }
+          af[i] = *reinterpret_cast<const i32x4*>(abase + i * 32 * kStage + a_frag_offset(t, lane));
         });
         i32x4 wf;
         if constexpr (PREP) {
           wf = i32x4{static_cast<int>(b.w[t][0]), static_cast<int>(b.w[t][1]), static_cast<int>(b.w[t][2]),
                      static_cast<int>(b.w[t][3])};
         } else {
-          const uint32_t c = b.cb[t / GK];
-          const uint32_t x0 = b.w[t][0] ^ xmask, x1 = b.w[t][1] ^ xmask;
-          wf = i32x4{static_cast<int>((x0 & 0x0F0F0F0Fu) + c), static_cast<int>(((x0 >> 4) & 0x0F0F0F0Fu) + c),
-                     static_cast<int>((x1 & 0x0F0F0F0Fu) + c), static_cast<int>(((x1 >> 4) & 0x0F0F0F0Fu) + c)};
+          const uint32_t zb = b.zb[t / GK];
+          auto expand = [&](uint32_t word, uint32_t& d0, uint32_t& d1) __attribute__((always_inline)) {
+            const uint32_t x = word ^ xmask;
+            const uint32_t lo = (((x & 0x0F0F0F0Fu) | 0x80808080u) - zb) ^ 0x80808080u;
+            const uint32_t hi = ((((x >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zb) ^ 0x80808080u;
+            d0 = __builtin_amdgcn_perm(hi, lo, sel0);
+            d1 = __builtin_amdgcn_perm(hi, lo, sel1);
+          };
+          uint32_t d[4];
+          expand(b.w[t][0], d[0], d[1]);
+          expand(b.w[t][1], d[2], d[3]);
+          wf = i32x4{static_cast<int>(d[0]), static_cast<int>(d[1]), static_cast<int>(d[2]), static_cast<int>(d[3])};
         }
         static_for<0, 4>([&](auto i_c) {
           constexpr int i = decltype(i_c)::value;

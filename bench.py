@@ -394,10 +394,15 @@ def main():
         sec["w4a8"] = run_w4a8(torch, dev)
         line["secondary"] = sec
     if not args.no_cpu_baseline:
-        from oracle.cpu_baseline import time_cfg1_chain
+        from oracle.cpu_baseline import cpu_model, time_cfg1_chain
         cpu_ops, cpu_s, threads, sample = time_cfg1_chain(rows=args.cpu_rows, seconds=args.cpu_seconds)
+        # the reference's own benchmark setting: 2 threads (bench_int8_gemm.py:54), a smaller sample
+        ops2, s2, _, sample2 = time_cfg1_chain(rows=min(512, args.cpu_rows), threads=2,
+                                               seconds=min(4.0, args.cpu_seconds))
         line["cpu_baseline"] = {"value": round(cpu_ops / 1e12, 4), "unit": "TOPS", "cores": threads,
-                                "kind": "port", "sample": sample, "seconds_per_sample": round(cpu_s, 3)}
+                                "kind": "port", "sample": sample, "seconds_per_sample": round(cpu_s, 3),
+                                "cpu_model": cpu_model(),
+                                "threads_2": {"value": round(ops2 / 1e12, 4), "unit": "TOPS", "sample": sample2}}
         if not args.no_secondary:
             from oracle.cpu_baseline import time_w4a16_decode
             gbs, sec_s, threads, sample = time_w4a16_decode(seconds=min(5.0, args.cpu_seconds))

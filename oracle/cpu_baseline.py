@@ -33,6 +33,18 @@ def w8a8_linear_cpu(x, wq_t, ws, bias, activation=None):
     return v.to(torch.float16)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def time_cfg1_chain(rows=4096, hidden=3072, threads=None, seconds=10.0, seed=1):
     """Time the cfg1 chain (QKV, up+GELU, down) on ``rows`` tokens on the CPU,
     repeating whole passes for about ``seconds`` (at least two).

@@ -6,8 +6,8 @@
 // fused path (rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:49-73, :195-206).
 //
 // Design:
-//  * one 256-thread workgroup (2 x 2 waves) per 128 x 128 output tile; each
-//    wave owns 64 x 64 as 4 x 4 fragments of v_mfma_f32_16x16x32_{bf16,f16};
+//  * one 512-thread workgroup (2 x 4 waves) per 128 x 128 output tile; each
+//    wave owns 64 x 32 as 4 x 2 fragments of v_mfma_f32_16x16x32_{bf16,f16};
 //  * K advances in 128-wide stages. The activation stage (128 rows x 256 B)
 //    is copied HBM -> LDS with global_load_lds_dwordx4 into a 2-slot ring,
 //    as two 128-byte-row halves with the 16-byte chunk index XOR-swizzled by
@@ -35,9 +35,14 @@ namespace {
 constexpr int kBM = 128, kBN = 128, kKS = 128;
 constexpr int kHalf = kBM * 128;            // bytes of one 64-wide K half of a stage
 constexpr int kStage = 2 * kHalf;           // 32 KB
-constexpr int kFM = 4, kFN = 4;             // 16x16 fragments per wave
 
 enum WdFormat { WD_W4_UINT4 = 0, WD_W4_GENERIC = 1, WD_FP8_E4M3 = 2, WD_FP8_E5M2 = 3 };
+
+// 8 waves as 2 x 4, 64 x 32 outputs each: half the accumulators and weight
+// registers of a 2 x 2 grid of 64 x 64 (two or three waves per SIMD instead
+// of one for W4; measured 1.26x on the cfg2 prefill, 1.1x on cfg3 N 3072);
+// 4 x 2 loads every weight column in four waves and is slower still.
+constexpr int kWdWavesM = 2;
 
 template <bool F16A>
 __device__ __forceinline__ f32x4 mfma16(const i32x4& a, const i32x4& b, const f32x4& c) {
@@ -132,16 +137,20 @@ __device__ __forceinline__ void put_out(void* out, int dtype, int64_t idx, float
 }
 
 // Weight registers of one stage for one wave: FN column tiles.
-template <int FMT>
+template <int FMT, int FN>
 struct StageW {
   static constexpr int R = (FMT >= WD_FP8_E4M3) ? 8 : 4;  // 32-bit words per lane per tile
-  uint32_t w[kFN][R];
-  uint32_t gs[kFN][4], gz[kFN][4];  // W4: raw scale / zero words per group slot
+  uint32_t w[FN][R];
+  uint32_t gs[FN][4], gz[FN][4];  // W4: raw scale / zero words per group slot
 };
 
-template <int FMT, int G, bool KN, bool F16A>
-__global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
+// NWM x NWN waves: each wave owns 16 kFM rows x 16 kFN columns of the
+// 128 x 128 tile, kFM = 8 / NWM, kFN = 8 / NWN.
+template <int FMT, int G, bool KN, bool F16A, int NWM, int NWN>
+__global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
 #pragma clang fp contract(off)
+  constexpr int NW = NWM * NWN;
+  constexpr int kFM = 8 / NWM, kFN = 8 / NWN;
   constexpr bool W4 = FMT <= WD_W4_GENERIC;
   constexpr bool UINT4 = FMT == WD_W4_UINT4;
   constexpr int SPS = W4 ? kKS / G : 1;         // W4 groups per stage
@@ -152,7 +161,7 @@ __global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wr = wave >> 1, wc = wave & 1;
+  const int wr = wave / NWN, wc = wave % NWN;
   const int col = lane & 15, q = lane >> 4;
 
   // ---- tile order: XCD-contiguous ranges, GROUP_M-swizzled inside --------
@@ -175,8 +184,8 @@ __global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
   const int S = p.K / kKS;
   auto dma_stage = [&](int s) {
     const uint32_t slot = smem_base + (s & 1) * kStage;
-    static_for<0, 8>([&](auto i) {
-      const int seg = wave + 4 * i;
+    static_for<0, 32 / NW>([&](auto i) {
+      const int seg = wave + NW * i;
       const int h = seg >> 4, rb = seg & 15;
       const int row = rb * 8 + srow;
       const uint32_t lc = static_cast<uint32_t>((lane & 7) ^ (row & 7));
@@ -189,9 +198,9 @@ __global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
 
   // ---- weight loads of one stage ----------------------------------------
   int ncol[kFN];
-  static_for<0, kFN>([&](auto t) { ncol[t] = min(n0 + wc * 64 + 16 * t + col, p.N - 1); });
+  static_for<0, kFN>([&](auto t) { ncol[t] = min(n0 + wc * 16 * kFN + 16 * t + col, p.N - 1); });
   const int KW = p.K >> 3;
-  auto load_w = [&](StageW<FMT>& sw, int s) {
+  auto load_w = [&](StageW<FMT, kFN>& sw, int s) {
     static_for<0, kFN>([&](auto t) {
       const uint32_t n = static_cast<uint32_t>(ncol[t]);
       if constexpr (!W4) {
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
   // chunk f = word_of(q, j) of the stage: half f >> 3, logical 16-byte chunk f & 7
   uint32_t a_row_off[kFM];
   static_for<0, kFM>([&](auto f) {
-    const int r = wr * 64 + 16 * f + col;
+    const int r = wr * 16 * kFM + 16 * f + col;
     a_row_off[f] = static_cast<uint32_t>(r * 128);
   });
   const int rsw = col & 7;  // (row & 7) of every row this lane reads
@@ -265,7 +274,7 @@ __global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
     });
   }
 
-  StageW<FMT> wcur, wnext;
+  StageW<FMT, kFN> wcur, wnext;
   if (S > 0) {
     dma_stage(0);
     load_w(wcur, 0);
@@ -330,13 +339,13 @@ __global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
 
   // ---- epilogue -------------------------------------------------------------
   static_for<0, kFN>([&](auto t) {
-    const int nn = n0 + wc * 64 + 16 * t + col;
+    const int nn = n0 + wc * 16 * kFN + 16 * t + col;
     if (nn < p.N) {
       const float bv = p.bias ? bias_at(p.bias, p.bias_dtype, nn) : 0.0f;
       const float ws = (!W4 && p.w_scale) ? p.w_scale[nn] : 1.0f;
       static_for<0, kFM>([&](auto f) {
         static_for<0, 4>([&](auto e) {
-          const int row = m0 + wr * 64 + 16 * f + 4 * q + e;
+          const int row = m0 + wr * 16 * kFM + 16 * f + 4 * q + e;
           if (row < p.M) {
             float v;
             if constexpr (W4) v = tot[f][t][int(e)];
@@ -356,10 +365,11 @@ __global__ __launch_bounds__(256, 1) void k_wd_gemm(WdArgs p) {
 template <int FMT, int G, bool KN>
 hipError_t launch_wd_t(const WdArgs& p, hipStream_t stream) {
   const int tiles = ceil_div(p.M, kBM) * ceil_div(p.N, kBN);
+  constexpr int NWM = kWdWavesM, NWN = 8 / kWdWavesM;
   if (p.a_f16)
-    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, true>), dim3(tiles), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, true, NWM, NWN>), dim3(tiles), dim3(64 * NWM * NWN), 0, stream, p);
   else
-    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, false>), dim3(tiles), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, false, NWM, NWN>), dim3(tiles), dim3(64 * NWM * NWN), 0, stream, p);
   return hipGetLastError();
 }
 

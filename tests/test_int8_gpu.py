@@ -41,8 +41,9 @@ def test_quant_rows_golden(cuda):
             assert np.array_equal(step.cpu().numpy().reshape(-1), d[f"step_{label}_{rounding}"])
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(4096, 3072), (33, 12288), (7, 100), (5, 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float8_e4m3fn,
+                                   torch.float8_e5m2])
+@pytest.mark.parametrize("shape", [(4096, 3072), (33, 12288), (7, 100), (5, 3), (3, 24576)])
 def test_quant_rows_random(cuda, dtype, shape):
     from rdna2_ops.quantize import quantize_int8_rowwise
     case(f"quant random {dtype} {shape}")
@@ -82,10 +83,11 @@ def _near_tie_rows(dtype, m, k, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("k", [4096, 20480])
+@pytest.mark.parametrize("k", [4096, 20480, 40960])
 def test_quant_rows_near_ties(cuda, dtype, k):
     """Bit-exact rounding of x / step at and next to half-integers, in the
-    register-resident kernel (k = 4096) and the two-pass kernel (k = 20480)."""
+    register-resident kernel (k = 4096, and k = 20480 for 2-byte inputs) and
+    the two-pass kernel (fp32 at k = 20480, every input at k = 40960)."""
     from rdna2_ops.quantize import quantize_int8_rowwise
     x = _near_tie_rows(dtype, 48, k, seed=k + 3)
     xf = x.float().numpy()

@@ -6,9 +6,10 @@
 //   q = clamp(round(x / step), -127, 127)    (round of the IEEE quotient)
 // Rows of up to 8 waves x 64 lanes x 6 16-byte chunks (24576 fp16) are loaded
 // into registers once, all loads in flight together, and quantized from there.
-// NW is the smallest of 1, 2, 4, 8 that leaves at most 3 chunks per lane: the
-// row's loads are spread over more waves (more requests in flight per CU, shorter
-// per-wave chains) — 25 us instead of 34 us for 4096 x 12288 fp16. The quotient is
+// NW is the smallest of 1, 2, 4, 8 that leaves at most 3 chunks per lane and NCH
+// the chunks per lane the row needs: the row's loads are spread over more
+// waves (more requests in flight per CU, shorter per-wave chains) — 25 us
+// instead of 34 us for 4096 x 12288 fp16. The quotient is
 // formed as x * rcp(step) (a few ulps from x / step); only when that lands
 // within 2^-12 of a rounding boundary (n + 1/2) is the IEEE division done, so
 // the rounded result is always that of the exact quotient. Longer or strided
@@ -115,9 +116,12 @@ __global__ __launch_bounds__(64 * NW) void k_quant_rows_reg(const char* x, int64
   }
   const float step = fmaxf(amax / 127.0f, 1.0e-20f);
   const float rstep = __builtin_amdgcn_rcpf(step);
-  // Decode again below rather than keep every decoded element live.
+  // Up to 3 chunks the decoded elements stay live (at most 48 registers);
+  // longer rows are decoded again rather than hold every element.
+  if constexpr (NCH > 3) {
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) asm volatile("" : "+v"(raw[i]));
+    for (int i = 0; i < NCH; ++i) asm volatile("" : "+v"(raw[i]));
+  }
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int c = t + T * i;
@@ -222,16 +226,22 @@ hipError_t launch_quant_t(const void* x, int64_t x_sm, int64_t x_sk, int64_t M, 
   const int m = static_cast<int>(M), k = static_cast<int>(K), kp = static_cast<int>(k_pad);
   if (vec && chunks <= 64 * 8 * 6) {
     const dim3 rows(static_cast<unsigned>(M));  // one row per workgroup
-    if (chunks <= 64 * 3)
-      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 1, 3>), rows, dim3(64), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
-    else if (chunks <= 128 * 3)
-      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 2, 3>), rows, dim3(128), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
-    else if (chunks <= 256 * 3)
-      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 4, 3>), rows, dim3(256), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
-    else if (chunks <= 512 * 3)
-      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 8, 3>), rows, dim3(512), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
-    else
-      hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, 8, 6>), rows, dim3(512), 0, stream, xp, x_sm, m, k, q, q_sm, kp, step);
+    // NW: the smallest of 1, 2, 4, 8 with at most 3 chunks per lane; NCH: the
+    // chunks per lane that row needs (1 to 3; 6 past 1536 chunks)
+#define QG_QUANT_REG(NW, NCH)                                                                   \
+  hipLaunchKernelGGL((k_quant_rows_reg<XT, MODE, NW, NCH>), rows, dim3(64 * NW), 0, stream, xp, \
+                     x_sm, m, k, q, q_sm, kp, step)
+    if (chunks <= 64) QG_QUANT_REG(1, 1);
+    else if (chunks <= 128) QG_QUANT_REG(1, 2);
+    else if (chunks <= 192) QG_QUANT_REG(1, 3);
+    else if (chunks <= 256) QG_QUANT_REG(2, 2);
+    else if (chunks <= 384) QG_QUANT_REG(2, 3);
+    else if (chunks <= 512) QG_QUANT_REG(4, 2);
+    else if (chunks <= 768) QG_QUANT_REG(4, 3);
+    else if (chunks <= 1024) QG_QUANT_REG(8, 2);
+    else if (chunks <= 1536) QG_QUANT_REG(8, 3);
+    else QG_QUANT_REG(8, 6);
+#undef QG_QUANT_REG
     return hipGetLastError();
   }
   if (vec)

@@ -43,7 +43,7 @@ def test_quant_rows_golden(cuda):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float8_e4m3fn,
                                    torch.float8_e5m2])
-@pytest.mark.parametrize("shape", [(4096, 3072), (33, 12288), (7, 100), (5, 3), (3, 24576)])
+@pytest.mark.parametrize("shape", [(4096, 3072), (33, 12288), (7, 100), (5, 3), (3, 24576), (9, 1024), (11, 2048)])
 def test_quant_rows_random(cuda, dtype, shape):
     from rdna2_ops.quantize import quantize_int8_rowwise
     case(f"quant random {dtype} {shape}")

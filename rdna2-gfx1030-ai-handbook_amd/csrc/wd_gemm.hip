@@ -6,12 +6,16 @@
 // fused path (rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:49-73, :195-206).
 //
 // Design:
-//  * one 512-thread workgroup (2 x 4 waves) per 128 x 128 output tile; each
-//    wave owns 64 x 32 as 4 x 2 fragments of v_mfma_f32_16x16x32_{bf16,f16};
+//  * one 512-thread workgroup (2 x 4 waves) per 128 x 128 output tile (FP8 on
+//    large grids: 256 x 128); each wave owns 64 x 32 (128 x 32) as 4 x 2
+//    (8 x 2) fragments of v_mfma_f32_16x16x32_{bf16,f16};
 //  * K advances in 128-wide stages. The activation stage (128 rows x 256 B)
 //    is copied HBM -> LDS with global_load_lds_dwordx4 into a 2-slot ring,
 //    as two 128-byte-row halves with the 16-byte chunk index XOR-swizzled by
-//    (row & 7) — the INT8 kernel's conflict-free layout;
+//    ((row >> 1) & 3) ^ 4 (row & 1). The fragment reads of a 16 x 16 x 32
+//    step (rows 0-15 at one logical chunk per lane quarter, quarters 2 and 3
+//    in the second half) measured 4 bank-conflict cycles per ds_read_b128
+//    with an XOR by (row & 7) or by ((row >> 1) & 7) and none with this one;
 //  * weights never touch LDS: each lane loads its column's words / bytes for
 //    the next stage into registers while the current stage computes, and
 //    expands them in registers right before the MFMA (nibble -> 128 + u or
@@ -24,7 +28,10 @@
 // copies of stage s (LDS) and its weight registers (vmcnt(0)), then the
 // workgroup barrier makes the whole stage visible and guarantees that the
 // other slot is free; stage s+1 is issued right after and overlaps stage s's
-// MFMAs.
+// MFMAs. Two stages per loop iteration with the weight register sets swapped
+// (no register copy, which would wait for the loads of stage s+1 at the end of
+// stage s): 126 -> 117 us for cfg3 N = 3072, 577 -> 558 us for the cfg2
+// prefill.
 #include "qg_common.h"
 #include "qg_internal.h"
 
@@ -32,9 +39,7 @@ namespace qg {
 
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kKS = 128;
-constexpr int kHalf = kBM * 128;            // bytes of one 64-wide K half of a stage
-constexpr int kStage = 2 * kHalf;           // 32 KB
+constexpr int kKS = 128;  // K elements per stage
 
 enum WdFormat { WD_W4_UINT4 = 0, WD_W4_GENERIC = 1, WD_FP8_E4M3 = 2, WD_FP8_E5M2 = 3 };
 
@@ -144,13 +149,18 @@ struct StageW {
   uint32_t gs[FN][4], gz[FN][4];  // W4: raw scale / zero words per group slot
 };
 
-// NWM x NWN waves: each wave owns 16 kFM rows x 16 kFN columns of the
-// 128 x 128 tile, kFM = 8 / NWM, kFN = 8 / NWN.
-template <int FMT, int G, bool KN, bool F16A, int NWM, int NWN>
+// TBM x TBN output tile, NWM x NWN waves: each wave owns 16 kFM rows x 16 kFN
+// columns, kFM = TBM / 16 / NWM, kFN = TBN / 16 / NWN.
+template <int FMT, int G, bool KN, bool F16A, int NWM, int NWN, int TBM, int TBN>
 __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
 #pragma clang fp contract(off)
   constexpr int NW = NWM * NWN;
-  constexpr int kFM = 8 / NWM, kFN = 8 / NWN;
+  constexpr int kFM = TBM / 16 / NWM, kFN = TBN / 16 / NWN;
+  constexpr int kBM = TBM, kBN = TBN;
+  constexpr int kHalf = kBM * 128;  // bytes of one 64-wide K half of an activation stage
+  constexpr int kStage = 2 * kHalf;
+  constexpr int kSegs = kBM / 4;    // 1 KB DMA segments (8 rows x 128 B) per stage
+  static_assert(kFM >= 1 && kFN >= 1 && kSegs % NW == 0, "tile / wave grid");
   constexpr bool W4 = FMT <= WD_W4_GENERIC;
   constexpr bool UINT4 = FMT == WD_W4_UINT4;
   constexpr int SPS = W4 ? kKS / G : 1;         // W4 groups per stage
@@ -177,21 +187,26 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
   const int m0 = (first + in_group % gm) * kBM;
   const int n0 = (in_group / gm) * kBN;
 
-  // ---- activation DMA plan: 32 segments (8 rows x 128 B) per stage --------
+  // ---- activation DMA plan: kSegs segments (8 rows x 128 B) per stage ------
   const int srow = lane >> 3;
   const uint32_t smem_base = lds_addr_of(smem);
   const char* a_base = reinterpret_cast<const char*>(p.a);
   const int S = p.K / kKS;
+  const uint32_t a_stride = static_cast<uint32_t>(2 * p.a_sm);
   auto dma_stage = [&](int s) {
     const uint32_t slot = smem_base + (s & 1) * kStage;
-    static_for<0, 32 / NW>([&](auto i) {
+    static_for<0, kSegs / NW>([&](auto i) {
       const int seg = wave + NW * i;
-      const int h = seg >> 4, rb = seg & 15;
+      const int h = seg / (kBM / 8), rb = seg % (kBM / 8);
       const int row = rb * 8 + srow;
-      const uint32_t lc = static_cast<uint32_t>((lane & 7) ^ (row & 7));
+      const uint32_t lc = static_cast<uint32_t>((lane & 7) ^ ((row >> 1) & 3) ^ (4 * (row & 1)));
       int rg = min(m0 + row, p.M - 1);
       asm volatile("" : "+v"(rg));
-      const uint32_t voff = static_cast<uint32_t>(rg) * static_cast<uint32_t>(2 * p.a_sm) + 128u * h + 16u * lc;
+      // a 32-bit product (the compiler would otherwise fold it into a 64-bit
+      // multiply-add and keep the per-segment constants in register pairs)
+      uint32_t roff;
+      asm("v_mul_lo_u32 %0, %1, %2" : "=v"(roff) : "v"(rg), "s"(a_stride));
+      const uint32_t voff = roff + 128u * h + 16u * lc;
       dma16s(a_base + static_cast<int64_t>(s) * 256, voff, slot + h * kHalf + rb * 1024);
     });
   };
@@ -252,7 +267,7 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
     const int r = wr * 16 * kFM + 16 * f + col;
     a_row_off[f] = static_cast<uint32_t>(r * 128);
   });
-  const int rsw = col & 7;  // (row & 7) of every row this lane reads
+  const int rsw = ((col >> 1) & 3) ^ (4 * (col & 1));  // swizzle of every row this lane reads
 
   uint32_t sel[4], umask = F16A ? 0x00F000F0u : 0x000F000Fu, umagic = F16A ? 0x5C005C00u : 0x43004300u;
   nat_selectors(W4 && !UINT4 && (p.flags & QG_W4_ORDER_HIGH), sel);
@@ -274,16 +289,14 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
     });
   }
 
-  StageW<FMT, kFN> wcur, wnext;
-  if (S > 0) {
-    dma_stage(0);
-    load_w(wcur, 0);
-  }
-  for (int s = 0; s < S; ++s) {
+  // Stage s computes from `cur` and loads stage s + 1 into `nxt`; the loop
+  // runs two stages per iteration with the register sets swapped, so no
+  // weight registers are copied (a copy would wait for the loads just issued).
+  auto stage = [&](int s, StageW<FMT, kFN>& cur, StageW<FMT, kFN>& nxt) __attribute__((always_inline)) {
     wait_vm_barrier<0>();  // stage s landed everywhere; slot (s+1)&1 is free
     if (s + 1 < S) {
       dma_stage(s + 1);
-      load_w(wnext, s + 1);
+      load_w(nxt, s + 1);
     }
     const char* const sbuf = smem + (s & 1) * kStage;
     static_for<0, 4>([&](auto j) {
@@ -303,8 +316,8 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
       if constexpr (W4) static_for<0, kFM>([&](auto f) { asum[f] = mfma16<F16A>(af[f], ones, asum[f]); });
       static_for<0, kFN>([&](auto t) {
         i32x4 b;
-        if constexpr (W4) b = unpack_nat<F16A>(wcur.w[t][j] ^ wxor, sel, umask, umagic);
-        else b = fp8x8<F16A, FMT == WD_FP8_E5M2>(wcur.w[t][2 * j], wcur.w[t][2 * j + 1]);
+        if constexpr (W4) b = unpack_nat<F16A>(cur.w[t][j] ^ wxor, sel, umask, umagic);
+        else b = fp8x8<F16A, FMT == WD_FP8_E5M2>(cur.w[t][2 * j], cur.w[t][2 * j + 1]);
         static_for<0, kFM>([&](auto f) { acc[f][t] = mfma16<F16A>(af[f], b, acc[f][t]); });
       });
       if constexpr (W4 && j % STEPS_PER_GROUP == STEPS_PER_GROUP - 1) {
@@ -313,7 +326,7 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
           const int g = s * SPS + gi;
           const uint32_t i = static_cast<uint32_t>(ncol[t]) * p.ng + g;
           float sc, zb;
-          const uint32_t rs = wcur.gs[t][gi], rz = wcur.gz[t][gi];
+          const uint32_t rs = cur.gs[t][gi], rz = cur.gz[t][gi];
           if constexpr (UINT4) {
             sc = __uint_as_float((i & 1u) ? (rs & 0xFFFF0000u) : (rs << 16));
             zb = MAGIC + UNIT * static_cast<float>((rz >> ((g & 7) * 4)) & 15u);
@@ -334,7 +347,15 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
         });
       }
     });
-    if (s + 1 < S) wcur = wnext;
+  };
+  StageW<FMT, kFN> w0, w1;
+  if (S > 0) {
+    dma_stage(0);
+    load_w(w0, 0);
+  }
+  for (int s = 0; s < S; s += 2) {
+    stage(s, w0, w1);
+    if (s + 1 < S) stage(s + 1, w1, w0);
   }
 
   // ---- epilogue -------------------------------------------------------------
@@ -362,15 +383,22 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
   });
 }
 
-template <int FMT, int G, bool KN>
-hipError_t launch_wd_t(const WdArgs& p, hipStream_t stream) {
-  const int tiles = ceil_div(p.M, kBM) * ceil_div(p.N, kBN);
+template <int FMT, int G, bool KN, int TBM, int TBN>
+hipError_t launch_wd_tile(const WdArgs& p, hipStream_t stream) {
+  const int tiles = ceil_div(p.M, TBM) * ceil_div(p.N, TBN);
   constexpr int NWM = kWdWavesM, NWN = 8 / kWdWavesM;
   if (p.a_f16)
-    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, true, NWM, NWN>), dim3(tiles), dim3(64 * NWM * NWN), 0, stream, p);
+    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, true, NWM, NWN, TBM, TBN>), dim3(tiles), dim3(64 * NWM * NWN), 0,
+                       stream, p);
   else
-    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, false, NWM, NWN>), dim3(tiles), dim3(64 * NWM * NWN), 0, stream, p);
+    hipLaunchKernelGGL((k_wd_gemm<FMT, G, KN, false, NWM, NWN, TBM, TBN>), dim3(tiles), dim3(64 * NWM * NWN), 0,
+                       stream, p);
   return hipGetLastError();
+}
+
+template <int FMT, int G, bool KN>
+hipError_t launch_wd_t(const WdArgs& p, hipStream_t stream) {
+  return launch_wd_tile<FMT, G, KN, 128, 128>(p, stream);
 }
 
 // dst[r, k] = src[r * s_r + k * s_k] (16-bit) for k < K, 0 for K <= k < k_pad.
@@ -419,9 +447,18 @@ hipError_t launch_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64
   return hipGetLastError();
 }
 
+// FP8: 256 x 128 tiles (wave tile 128 x 32; 1.3x fewer bytes per MFMA than
+// 128 x 128, one workgroup per CU for its 128 KB of activation ring) once the
+// grid has at least four of them per CU: 397 us against 474 us for cfg3's
+// N = 12288, while N = 3072 (1.5 such tiles per CU) stays faster at 128 x 128
+// (117 us against 131 us). 256 x 256 spills and W4 does not fit either.
 hipError_t launch_wd_fp8(const WdArgs& p, hipStream_t stream) {
-  return p.fp8_e5 ? launch_wd_t<WD_FP8_E5M2, 128, false>(p, stream)
-                  : launch_wd_t<WD_FP8_E4M3, 128, false>(p, stream);
+  const int64_t wide_tiles = static_cast<int64_t>(ceil_div(p.M, 256)) * ceil_div(p.N, 128);
+  if (p.M >= 256 && wide_tiles >= 4 * 256)
+    return p.fp8_e5 ? launch_wd_tile<WD_FP8_E5M2, 128, false, 256, 128>(p, stream)
+                    : launch_wd_tile<WD_FP8_E4M3, 128, false, 256, 128>(p, stream);
+  return p.fp8_e5 ? launch_wd_tile<WD_FP8_E5M2, 128, false, 128, 128>(p, stream)
+                  : launch_wd_tile<WD_FP8_E4M3, 128, false, 128, 128>(p, stream);
 }
 
 hipError_t launch_wd_w4(const WdArgs& p, hipStream_t stream) {

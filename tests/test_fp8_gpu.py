@@ -177,6 +177,31 @@ def test_contract_errors(cuda):
         m_.decode_fp8_weight(w, out_dtype=torch.int8)
 
 
+@pytest.mark.parametrize("e5", [False, True])
+def test_fused_wide_tiles_ragged(cuda, e5):
+    """Grids large enough for the 256 x 128 tiles (at least four per CU) with
+    ragged M (1000 = 3 x 256 + 232) and N (32800 = 256 x 128 + 32); rows on
+    both sides of every M tile edge are checked against float64."""
+    m, n, k = 1000, 32800, 256
+    case(f"fp8 fused wide tiles m{m} n{n} k{k} e5={e5}")
+    rng = np.random.default_rng(17 + e5)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    if e5:
+        codes = torch.from_numpy(wf / 0.02 * 4).to(torch.float8_e5m2).view(torch.uint8).numpy()
+        s = (rng.random(n) * 0.01 + 0.001).astype(np.float32)
+    else:
+        codes, s = o8.quantize_weight_per_channel(wf)
+    a = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    b = torch.from_numpy((rng.standard_normal(n) * 0.1).astype(np.float32)).to(torch.bfloat16)
+    y = mod().fp8_weight_gemm(a.to(cuda), codes_tensor(codes, e5, cuda), bias=b.to(cuda), method="fused_dot2",
+                              w_scale=torch.from_numpy(s).to(cuda))
+    rows = np.array([0, 1, 127, 128, 255, 256, 511, 512, 767, 768, 900, 998, 999])
+    av = a.float().numpy().astype(np.float64)[rows]
+    y64 = o8.fp8_linear(av, codes, s, b.float().numpy(), e5)
+    absdot = o8.fp8_linear(np.abs(av), codes & 0x7F, s, None, e5)
+    check(y[torch.from_numpy(rows).to(cuda)], y64, absdot, torch.bfloat16, f"wide tiles e5={e5}")
+
+
 @pytest.mark.parametrize("n", [3072, 12288])
 def test_cfg3_full_size(cuda, n):
     """BASELINE configuration 3 at its real shape: M 4096, K 3072, e4m3

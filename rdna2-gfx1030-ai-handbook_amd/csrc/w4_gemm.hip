@@ -229,7 +229,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_skinny(W4Args p) {
                       static_cast<int>(ones2)};
 
   // byte offset of word kw of column n
-  auto woff = [&](int n, int kw) -> uint32_t {
+  auto woff = [&](int n, int kw) __attribute__((always_inline)) -> uint32_t {
     return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (static_cast<uint32_t>(n) * KW + kw);
   };
   uint32_t arow_off[FM];
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_skinny(W4Args p) {
     arow_off[f] = 2u * static_cast<uint32_t>(min(m0 + 16 * f + col, p.M - 1)) * static_cast<uint32_t>(p.a_sm);
   });
 
-  auto load = [&](SkinnyChunk<FM, CT, SPC>& ch, int c) {
+  auto load = [&](SkinnyChunk<FM, CT, SPC>& ch, int c) __attribute__((always_inline)) {
     const int kw0 = c * 16;
     static_for<0, CT>([&](auto t) {
       const int n = ncol[t];
@@ -274,7 +274,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_skinny(W4Args p) {
   // Straight-line: all 4 steps of every scheduled chunk run on (clamped)
   // data; a group that does not exist — past K, or a refill past the wave's
   // last chunk — gets scale 0 and adds exactly 0 (inputs are finite).
-  auto compute = [&](const SkinnyChunk<FM, CT, SPC>& ch, int c) {
+  auto compute = [&](const SkinnyChunk<FM, CT, SPC>& ch, int c) __attribute__((always_inline)) {
     const bool live = c <= clast;
     static_for<0, 4>([&](auto j) {
       {
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
   const uint32_t wxor = (!UINT4 && (p.flags & QG_W4_SIGNED_NIBBLES)) ? 0x88888888u : 0u;
   const i32x4 ones = {static_cast<int>(ones2), static_cast<int>(ones2), static_cast<int>(ones2),
                       static_cast<int>(ones2)};
-  auto woff = [&](int n, int kw) -> uint32_t {
+  auto woff = [&](int n, int kw) __attribute__((always_inline)) -> uint32_t {
     return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (static_cast<uint32_t>(n) * KW + kw);
   };
 
@@ -685,7 +685,9 @@ __global__ void k_w4_unpack(W4Args p) {
 
 template <int FM, int CT, int G, bool KN, bool F16A>
 hipError_t launch_skinny_t(const W4Args& p, hipStream_t stream) {
-  constexpr int DEPTH = (FM * CT <= 2) ? 4 : 2;
+  // chunks in flight per wave; groups of 64 / 32 hold 2 / 4 scale and zero
+  // words per column and chunk, so they keep half as many (no spills)
+  constexpr int DEPTH = G == 128 ? ((FM * CT <= 2) ? 4 : 2) : ((FM * CT <= 2) ? 2 : 1);
   constexpr int WAVES = 8;
   dim3 grid(ceil_div(p.N, 16 * CT), ceil_div(p.M, 16 * FM));
   constexpr int kUint4Flags = QG_W4_ZEROS_PACKED;
@@ -732,9 +734,9 @@ hipError_t launch_decode_g(const W4Args& p, hipStream_t stream) {
     case 64:
       return kn ? launch_decode_t<RP, 2, 64, true, F16A, false>(p, stream)
                 : launch_decode_t<RP, 2, 64, false, F16A, false>(p, stream);
-    default:
-      return kn ? launch_decode_t<RP, 2, 32, true, F16A, false>(p, stream)
-                : launch_decode_t<RP, 2, 32, false, F16A, false>(p, stream);
+    default:  // group 32: one column tile per wave past one row (4 scale / zero words per chunk)
+      return kn ? launch_decode_t<RP, (RP > 1 ? 1 : 2), 32, true, F16A, false>(p, stream)
+                : launch_decode_t<RP, (RP > 1 ? 1 : 2), 32, false, F16A, false>(p, stream);
   }
 }
 

@@ -193,7 +193,7 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
   const char* a_base = reinterpret_cast<const char*>(p.a);
   const int S = p.K / kKS;
   const uint32_t a_stride = static_cast<uint32_t>(2 * p.a_sm);
-  auto dma_stage = [&](int s) {
+  auto dma_stage = [&](int s) __attribute__((always_inline)) {
     const uint32_t slot = smem_base + (s & 1) * kStage;
     static_for<0, kSegs / NW>([&](auto i) {
       const int seg = wave + NW * i;
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
   int ncol[kFN];
   static_for<0, kFN>([&](auto t) { ncol[t] = min(n0 + wc * 16 * kFN + 16 * t + col, p.N - 1); });
   const int KW = p.K >> 3;
-  auto load_w = [&](StageW<FMT, kFN>& sw, int s) {
+  auto load_w = [&](StageW<FMT, kFN>& sw, int s) __attribute__((always_inline)) {
     static_for<0, kFN>([&](auto t) {
       const uint32_t n = static_cast<uint32_t>(ncol[t]);
       if constexpr (!W4) {
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(64 * NWM * NWN, 1) void k_wd_gemm(WdArgs p) {
         });
       } else {
         const int kw0 = 16 * s;
-        auto woff = [&](int kw) -> uint32_t {
+        auto woff = [&](int kw) __attribute__((always_inline)) -> uint32_t {
           return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (n * KW + kw);
         };
         if constexpr (!KN && G == 128) {

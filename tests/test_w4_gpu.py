@@ -115,7 +115,7 @@ def _gemm_case(cuda, m, n, k, g, sym, layout, order, adtype, bias, out_dtype=Non
 @pytest.mark.parametrize("layout,order", [("nk", "low"), ("nk", "high"), ("kn", "low"), ("kn", "high")])
 @pytest.mark.parametrize("adtype", [torch.float16, torch.bfloat16])
 def test_w4a16_small_all_formats(cuda, g, layout, order, adtype):
-    for m, sym, bias in ((1, False, True), (7, True, False), (16, False, False), (37, False, True)):
+    for m, sym, bias in ((1, False, True), (3, True, True), (7, True, False), (16, False, False), (37, False, True)):
         case(f"w4a16 m{m} n53 k384 g{g} {layout} {order} {adtype} sym={sym}")
         _gemm_case(cuda, m, 53, 384, g, sym, layout, order, adtype, bias, seed=m + g)
 

@@ -157,10 +157,9 @@ __device__ __forceinline__ void store_elem(void* out, int64_t idx, uint32_t bits
 // of the 8 XCDs (round-robin workgroup dispatch) walks one contiguous range of
 // tiles, GROUP_M-ordered inside.
 template <int BM, int BN>
-__device__ __forceinline__ void tile_origin(const I8GemmArgs& p, int& m0, int& n0) {
+__device__ __forceinline__ void tile_origin_at(const I8GemmArgs& p, int bid, int& m0, int& n0) {
   const int nbm = ceil_div(p.M, BM), nbn = ceil_div(p.N, BN);
   const int total = nbm * nbn;
-  int bid = blockIdx.x;
   if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
   constexpr int GROUP_M = 4;
   const int group = bid / (GROUP_M * nbn);
@@ -169,6 +168,10 @@ __device__ __forceinline__ void tile_origin(const I8GemmArgs& p, int& m0, int& n
   const int in_group = bid - group * GROUP_M * nbn;
   m0 = (first + in_group % gm) * BM;
   n0 = (in_group / gm) * BN;
+}
+template <int BM, int BN>
+__device__ __forceinline__ void tile_origin(const I8GemmArgs& p, int& m0, int& n0) {
+  tile_origin_at<BM, BN>(p, static_cast<int>(blockIdx.x), m0, n0);
 }
 
 // Copies of one operand: segment i of a wave covers 8 rows starting at row
@@ -502,14 +505,15 @@ constexpr int pp_copies() { return (G::BM > G::BN ? G::BM : G::BN) / 32; }
 // chunk; a_base / w_base point at K = 0. park() runs in every wave once its
 // first copies, and every load it issued before the loop, have landed, and
 // before the barrier that opens the loop: it parks the epilogue parameters in
-// LDS. On return no copy is in flight and every wave has passed the barrier
-// after the last read of the rings, so each wave may stage its epilogue in its
-// own part of the rings at once (group X's epilogue overlaps group Y's last
-// MFMAs).
+// LDS. With `pre`, this wave's stage-0 copies (W(0) for X, A(0) for Y) were
+// already issued by pp_prefetch0 (during the previous tile's epilogue). On
+// return no copy is in flight and every wave has passed the barrier after the
+// last read of the rings, so each wave may stage its epilogue in its own part
+// of the rings at once (group X's epilogue overlaps group Y's last MFMAs).
 template <typename G, typename Park>
 __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* smem, const char* a_base,
                                             const char* w_base, const uint32_t (&voff)[pp_copies<G>()], int S,
-                                            int wave, int lane, Park&& park) {
+                                            int wave, int lane, bool pre, Park&& park) {
   static_assert(G::NW == 8 && G::NA == 3 && G::KT == 4, "ping-pong geometry");
   constexpr int XS = G::BN / 32, YS = G::BM / 32;  // copies per wave and stage (W by X, A by Y)
   const int wr = wave / G::WGN, wc = wave % G::WGN;
@@ -579,7 +583,7 @@ __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* s
   // B1 of every stage.
   if (grp_x) {
     // prologue: W(0) landed everywhere, then read stage 0 and copy W(1)
-    static_for<0, XS>([&](auto d) { copy_w(d, 0); });
+    if (!pre) static_for<0, XS>([&](auto d) { copy_w(d, 0); });
     wait_vm<0>();
     park();
     wait_lds_barrier();
@@ -593,7 +597,7 @@ __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* s
       else if (s + 1 < S) load_phase(T_{}, F_{}, s + 1, 0);
     }
   } else {
-    static_for<0, YS>([&](auto d) { copy_a(d, 0); });
+    if (!pre) static_for<0, YS>([&](auto d) { copy_a(d, 0); });
     if (S > 1) {
       static_for<0, YS>([&](auto d) { copy_a(d, 1); });
       wait_vm<YS>();
@@ -616,6 +620,28 @@ __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* s
   }
 }
 
+// Stage-0 copies of the next tile (W(0) by group X into W slot 0, A(0) by group
+// Y into A slot 0), issued once pp_mainloop has returned for the current tile:
+// the rings are no longer read, and the epilogue stages outside these slots.
+template <typename G>
+__device__ __forceinline__ void pp_prefetch0(char* smem, const char* a_base, const char* w_base,
+                                             const uint32_t (&voff)[pp_copies<G>()], int wave) {
+  constexpr int XS = G::BN / 32, YS = G::BM / 32;
+  const int gw = wave & 3;
+  const uint32_t smem_base = lds_addr_of(smem);
+  if (wave < 4) {
+    static_for<0, XS>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      dma16s(w_base, voff[I], smem_base + G::RING_B + (gw + 4 * I) * 1024);
+    });
+  } else {
+    static_for<0, YS>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      dma16s(a_base, voff[I], smem_base + (gw + 4 * I) * 1024);
+    });
+  }
+}
+
 // Two fp32 values rounded to nearest-even fp16 / bf16 and packed (first in the
 // low half) by one paired hardware conversion; bit-identical to f32_to_f16 /
 // f32_to_bf16 for every fp32 input, NaNs included.
@@ -633,7 +659,7 @@ __device__ __forceinline__ f32x4 col4(const float* v, int c0) { return *reinterp
 // column scales and fp32 bias values parked at SC_A, SC_B and SC_BIAS).
 // Full tiles are staged per wave in its own part of the rings and leave as
 // whole 16-byte row chunks; edge tiles store element-wise.
-template <typename G, int OUT, int MODE>
+template <typename G, int OUT, int MODE, int STAGE_BASE = 0, int REGION = G::RING / G::NW>
 __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const i32x16 (&acc)[G::FM][G::FN], char* smem,
                                             int m0, int n0, int wr, int wc, int wave, int lane) {
 #pragma clang fp contract(off)
@@ -679,11 +705,10 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const i32x16 (&
   if (full) {
     // PF blocks of 32 rows per pass through the wave's staging region
     constexpr int ROWB = G::WN * ES + 16;  // padded LDS row pitch
-    constexpr int REGION = G::RING / G::NW;
     constexpr int PF = (G::FM * 32 * ROWB <= REGION) ? G::FM : (G::FM / 2 * 32 * ROWB <= REGION) ? G::FM / 2 : 1;
     static_assert(PF * 32 * ROWB <= REGION && G::FM % PF == 0, "epilogue staging does not fit");
     constexpr int CHUNKS = G::WN * ES / 16;  // 16-byte chunks per row
-    char* region = smem + wave * REGION;
+    char* region = smem + STAGE_BASE + wave * REGION;
     char* out = static_cast<char*>(p.out);
     static_for<0, G::FM / PF>([&](auto pass) {
       static_for<0, G::FN>([&](auto j) {
@@ -738,10 +763,20 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const i32x16 (&
   }
 }
 
+// Persistent: workgroup b computes tiles b, b + gridDim.x, ... (the grid is at
+// most one workgroup per CU, and every wave of a workgroup takes the same tiles,
+// so all waves pass the same barriers). With 2-byte outputs the next tile's
+// stage-0 copies (A slot 0, W slot 0) are issued before the current tile's
+// epilogue, which stages in A slots 1-2, so the next tile's first copy latency
+// overlaps the epilogue; a barrier after the epilogue keeps the next tile's
+// parked parameters and stage-1 copies off the LDS the epilogue still reads.
 template <typename G, int OUT, int MODE>
 __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
 #pragma clang fp contract(off)
   constexpr int YS = pp_copies<G>();
+  constexpr bool PREF = out_size<OUT>() == 2;
+  constexpr int EPI_BASE = PREF ? G::STAGE_A : 0;
+  constexpr int EPI_REGION = PREF ? (G::NA - 1) * G::STAGE_A / G::NW : G::RING / G::NW;
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
 
   const int tid = threadIdx.x;
@@ -749,38 +784,71 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave / G::WGN, wc = wave % G::WGN;
   const bool grp_x = wave < 4;
-  int m0, n0;
-  tile_origin<G::BM, G::BN>(p, m0, n0);
-  const EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
+  const int total = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
+  const int S = p.K / G::KS;
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  const char* w_base = reinterpret_cast<const char*>(p.w);
 
   // Copy i of a wave covers rows 8 (gw + 4 i) .. + 7 of its operand's tile;
-  // the 32-bit row offsets (clamped rows, swizzled chunk) are computed once.
-  const CopyPlan<4> plan(grp_x ? n0 : m0, wave & 3, lane);
+  // the 32-bit row offsets (clamped rows, swizzled chunk) are computed once
+  // per tile.
   uint32_t voff[YS];
-  {
+  auto plan_offsets = [&](int m0_, int n0_) __attribute__((always_inline)) {
+    const CopyPlan<4> plan(grp_x ? n0_ : m0_, wave & 3, lane);
     const int rows = grp_x ? p.N : p.M;
     const uint32_t stride = static_cast<uint32_t>(grp_x ? p.w_sn : p.a_sm);
     static_for<0, YS>([&](auto i_c) {
       constexpr int I = decltype(i_c)::value;
       voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, rows - 1)) * stride + plan.chunk16;
     });
-  }
-  i32x16 acc[G::FM][G::FN];
-  static_for<0, G::FM>([&](auto i) {
-    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
-  });
-  auto park = [&]() {
-    if constexpr (MODE != EPI_INT) {
-      if (tid < G::BM) reinterpret_cast<float*>(smem + G::SC_A)[tid] = ep.sa;
-      if (tid < G::BN) {
-        reinterpret_cast<float*>(smem + G::SC_B)[tid] = ep.sb;
-        reinterpret_cast<float*>(smem + G::SC_BIAS)[tid] = bias_value(ep.bias, p.bias_dtype);
-      }
-    }
   };
-  pp_mainloop<G>(acc, smem, reinterpret_cast<const char*>(p.a), reinterpret_cast<const char*>(p.w), voff,
-                 p.K / G::KS, wave, lane, park);
-  pp_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane);
+
+  int t = blockIdx.x;
+  int m0, n0;
+  tile_origin_at<G::BM, G::BN>(p, t, m0, n0);
+  EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
+  plan_offsets(m0, n0);
+  bool pre = false;
+  i32x16 acc[G::FM][G::FN];
+  for (;;) {
+    // The lane index passes through an opaque copy per tile: lane-derived LDS
+    // and global offsets of the main loop and the epilogue are then recomputed
+    // per tile instead of being hoisted out of the tile loop (which needs more
+    // registers than the main loop leaves free).
+    int lane_t = lane;
+    asm volatile("" : "+v"(lane_t));
+    static_for<0, G::FM>([&](auto i) {
+      static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
+    });
+    auto park = [&]() __attribute__((always_inline)) {
+      if constexpr (MODE != EPI_INT) {
+        if (tid < G::BM) reinterpret_cast<float*>(smem + G::SC_A)[tid] = ep.sa;
+        if (tid < G::BN) {
+          reinterpret_cast<float*>(smem + G::SC_B)[tid] = ep.sb;
+          reinterpret_cast<float*>(smem + G::SC_BIAS)[tid] = bias_value(ep.bias, p.bias_dtype);
+        }
+      }
+    };
+    pp_mainloop<G>(acc, smem, a_base, w_base, voff, S, wave, lane_t, pre, park);
+    const int tn = t + static_cast<int>(gridDim.x);
+    const bool more = tn < total;
+    int m1 = 0, n1 = 0;
+    EpiParams ep1;
+    if (more) {
+      tile_origin_at<G::BM, G::BN>(p, tn, m1, n1);
+      ep1 = fetch_epi_params<G::BM, G::BN, MODE>(p, m1, n1, tid);
+      plan_offsets(m1, n1);
+      if (PREF && S > 0) pp_prefetch0<G>(smem, a_base, w_base, voff, wave);
+    }
+    pp_epilogue<G, OUT, MODE, EPI_BASE, EPI_REGION>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
+    if (!more) break;
+    wait_lds_barrier();
+    t = tn;
+    m0 = m1;
+    n0 = n1;
+    ep = ep1;
+    pre = PREF && S > 0;
+  }
 }
 
 __device__ __forceinline__ float silu(float g) {
@@ -879,7 +947,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
   };
   pp_mainloop<G>(acc, smem, reinterpret_cast<const char*>(p.a),
                  reinterpret_cast<const char*>(p.w) + static_cast<int64_t>(e) * p.w_estride, voff, p.K / G::KS,
-                 wave, lane, park);
+                 wave, lane, false, park);
 
   // ---- epilogue -------------------------------------------------------------
   const int lr = lane & 31, lq = 4 * (lane >> 5);
@@ -998,14 +1066,18 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
   }
 }
 
+// CUs of an MI355X (gfx950): the persistent grid size.
+constexpr int kPersistentCUs = 256;
+
 template <typename G, int WPE, int OUT, int MODE>
 hipError_t launch_tile(const I8GemmArgs& p, hipStream_t stream) {
   static_assert(G::LDS_BYTES * WPE <= 160 * 1024, "LDS per CU");
   const int blocks = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
   if constexpr (G::NW == 4)
     hipLaunchKernelGGL((k_i8_gemm<G, WPE, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
-  else
-    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
+  else  // persistent: at most one workgroup per CU (LDS), a multiple of the 8 XCDs
+    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE>), dim3(blocks < kPersistentCUs ? blocks : kPersistentCUs),
+                       dim3(G::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -373,7 +373,7 @@ def main():
                    "tokens": chain.m, "hidden": 3072, "ops_per_step": ops},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS,
                      "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_bytes(),
-                     "kernel": "k_i8_gemm_pp<256x192 tile, 8 waves> (int8 MFMA GEMM, ping-pong main loop, fused epilogue)",
+                     "kernel": "k_i8_gemm_pp<256x192 tile, 8 waves> (int8 MFMA GEMM, ping-pong main loop, fused epilogue, persistent grid)",
                      "per_launch": layer_info},
     }
     if not args.no_secondary:

@@ -182,12 +182,15 @@ def _bits(x, out):
     return enc.view(np.uint32) if out == "f32" else enc.view(np.uint16)
 
 
-@pytest.mark.parametrize("m,n,k", [(4000, 3000, 384), (4096, 3072, 128), (4096, 3072, 256), (3841, 2881, 512)])
+@pytest.mark.parametrize("m,n,k", [(4000, 3000, 384), (4096, 3072, 128), (4096, 3072, 256), (3841, 2881, 512),
+                                   (4000, 9000, 256), (4096, 4608, 0)])
 def test_int8_pingpong_edges_and_epilogues(cuda, m, n, k):
     """Shapes of >= 192 tiles of 256 x 192, i.e. the 8-wave ping-pong kernel:
     edge tiles in both dimensions, one and two K stages, rows whose byte length
-    is not a multiple of 16 (element-wise stores). int32 and every epilogue
-    order / output dtype bit-exact against the oracle."""
+    is not a multiple of 16 (element-wise stores), more tiles than workgroups
+    of the persistent grid (752 and 384 tiles on 256 workgroups, the first
+    ragged in both dimensions) and K = 0. int32 and every epilogue order /
+    output dtype bit-exact against the oracle."""
     from rdna2_ops.int8_gemm import int8_gemm_dequant, int8_matmul
     case(f"int8 ping-pong {m}x{n}x{k}")
     g = torch.Generator().manual_seed(m + 3 * n + 7 * k)

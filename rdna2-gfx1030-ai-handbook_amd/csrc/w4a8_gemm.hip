@@ -43,14 +43,23 @@ namespace {
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBM = 128, kBN = 128, kThreads = 256;
+constexpr int kBM = 128;
 constexpr int kStage = 128;                       // K bytes per stage
 constexpr int kSlotA = kBM * kStage;              // 16 KB per A slot
-constexpr int kSlotS = 4 * kBN * 4;               // <= 4 groups x 128 fp32 scales
-constexpr int kLds = 2 * kSlotA + 2 * kSlotS;     // 36 KB
+
+// NW waves own 32 output columns each: a 128 x 32 NW tile, one A stage in LDS
+// shared by all of them.
+template <int NW>
+struct W8Geo {
+  static constexpr int BN = 32 * NW, THREADS = 64 * NW;
+  static constexpr int SLOT_S = 4 * BN * 4;       // <= 4 groups x BN fp32 scales
+  static constexpr int LDS = 2 * kSlotA + 2 * SLOT_S;
+  static_assert(16 % NW == 0, "A copies split evenly over the waves");
+};
 
 // Output tile of this workgroup (same XCD-aware, GROUP_M-ordered walk as the
 // INT8 GEMM).
+template <int kBN>
 __device__ __forceinline__ void w4a8_tile(int M, int N, int& m0, int& n0) {
   const int nbm = ceil_div(M, kBM), nbn = ceil_div(N, kBN);
   const int total = nbm * nbn;
@@ -80,40 +89,43 @@ struct WStage {
   uint32_t zb[4];
 };
 
-template <int G, bool PREP, bool INTEGER>
-__global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
+template <int G, bool PREP, bool INTEGER, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
 #pragma clang fp contract(off)
   constexpr int GK = G / 32;      // k-steps per group
   constexpr int GS = kStage / G;  // groups per stage
-  __shared__ __attribute__((aligned(1024))) char smem[kLds];
+  constexpr int kBN = W8Geo<NW>::BN;
+  constexpr int kSlotS = W8Geo<NW>::SLOT_S;
+  constexpr int NA = 16 / NW;     // A copies (1 KB each) per wave and stage
+  __shared__ __attribute__((aligned(1024))) char smem[W8Geo<NW>::LDS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, lr = lane & 31;
   int m0, n0;
-  w4a8_tile(p.M, p.N, m0, n0);
+  w4a8_tile<kBN>(p.M, p.N, m0, n0);
   const int KT = p.K / 32;                 // k-steps
   const int S = ceil_div(p.K, kStage);     // stages
   const uint32_t smem_base = lds_addr_of(smem);
 
-  // ---- A copies: copy I of this wave covers tile rows 8 (wave + 4 I) .. + 7;
+  // ---- A copies: copy I of this wave covers tile rows 8 (wave + NW I) .. + 7;
   // lane l fetches logical chunk (l & 7) ^ ((row >> 1) & 7) of its row, rows
   // clamped into A, and in a last partial stage chunks past K fetch chunk 0
   // (their LDS bytes are never read).
   const uint32_t chunk = static_cast<uint32_t>(((lane & 7) ^ (4 * (wave & 1) + (lane >> 4))) << 4);
   const uint32_t klast = static_cast<uint32_t>(p.K - (S - 1) * kStage);
-  uint32_t aoff[4];
-  for (int i = 0; i < 4; ++i)
-    aoff[i] = static_cast<uint32_t>(min(m0 + wave * 8 + (lane >> 3) + 32 * i, p.M - 1)) *
+  uint32_t aoff[NA];
+  for (int i = 0; i < NA; ++i)
+    aoff[i] = static_cast<uint32_t>(min(m0 + wave * 8 + (lane >> 3) + 8 * NW * i, p.M - 1)) *
               static_cast<uint32_t>(p.a_sm);
   const char* a_base = reinterpret_cast<const char*>(p.a);
   auto copy_a = [&](int s, int slot) __attribute__((always_inline)) {
     const uint32_t ch = (s == S - 1 && chunk >= klast) ? 0u : chunk;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NA; ++i)
       dma16s(a_base + static_cast<int64_t>(s) * kStage, aoff[i] + ch,
-             smem_base + slot * kSlotA + (wave + 4 * i) * 1024);
+             smem_base + slot * kSlotA + (wave + NW * i) * 1024);
   };
 
   // ---- this lane's weight row (output column n0 + 32 wave + (l & 31))
@@ -164,9 +176,9 @@ __global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
     }
   };
 
-  // ---- scales of a stage: thread t covers column t & 127 and the stage's
-  // groups (t >> 7) and (t >> 7) + 2 (clamped; only valid ones are stored)
-  const int scol = tid & (kBN - 1), sg0 = tid >> 7;
+  // ---- scales of a stage: thread t covers column t % BN and the stage's
+  // groups t / BN and t / BN + 2 (clamped; only valid ones are stored)
+  const int scol = tid & (kBN - 1), sg0 = tid / kBN;
   const int scn = min(n0 + scol, p.N - 1);
   auto load_scales = [&](int s, float (&sc)[2]) __attribute__((always_inline)) {
     if constexpr (!INTEGER) {
@@ -335,13 +347,20 @@ __global__ __launch_bounds__(kThreads, 2) void k_w4a8(W4A8Args p) {
   });
 }
 
+// 4 waves (two workgroups per CU): 8 waves on 128 x 256 tiles halve the A
+// bytes per MAC but took 187 us against 145 us on (4096, 3072, 3072) g128 and
+// 105 against 82 us on (1061, 3072, 3072) g32 (one workgroup per CU: the
+// per-stage barrier then stalls every wave of the CU at once).
+constexpr int kW4A8Waves = 4;
+
 template <int G, bool PREP>
 hipError_t launch_g(const W4A8Args& p, hipStream_t stream) {
-  const int blocks = ceil_div(p.M, kBM) * ceil_div(p.N, kBN);
+  constexpr int NW = kW4A8Waves;
+  const int blocks = ceil_div(p.M, kBM) * ceil_div(p.N, W8Geo<NW>::BN);
   if (p.integer)
-    hipLaunchKernelGGL((k_w4a8<G, PREP, true>), dim3(blocks), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((k_w4a8<G, PREP, true, NW>), dim3(blocks), dim3(W8Geo<NW>::THREADS), 0, stream, p);
   else
-    hipLaunchKernelGGL((k_w4a8<G, PREP, false>), dim3(blocks), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((k_w4a8<G, PREP, false, NW>), dim3(blocks), dim3(W8Geo<NW>::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -656,30 +656,78 @@ __global__ void k_w4_pack(W4PackArgs p) {
 }
 
 // out[n, k] = (q - z) (int8) or (q - z) * s rounded once to the output dtype
-// (_unpack_weight, int4_weight_gemm_v07.py:136-151).
-__global__ void k_w4_unpack(W4Args p) {
-  const int64_t total = static_cast<int64_t>(p.N) * p.K;
-  const int ng = p.K / p.group;
+// (_unpack_weight, int4_weight_gemm_v07.py:136-151). One thread per 4 packed
+// words of a column (32 K elements: K and the group are multiples of 32, so
+// they share one group): the scale and zero point are read once and the 32
+// outputs leave as 8- to 32-byte stores (element stores when `vec` is 0, an
+// output base that does not allow them). Threads walk the quads in storage
+// order (n fastest for the kn layout), so word loads are coalesced.
+template <int OUT>
+__global__ __launch_bounds__(256) void k_w4_unpack(W4Args p, int vec) {
+  const int KW = p.K >> 3, KQ = KW >> 2;  // words and word quads per column
+  const int quads = p.N * KQ;              // < 2^28 (N K < 2^31)
+  const bool kn = p.flags & QG_W4_LAYOUT_KN;
   const bool sgn = p.flags & QG_W4_SIGNED_NIBBLES;
   const bool high = p.flags & QG_W4_ORDER_HIGH;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int n = static_cast<int>(i / p.K), k = static_cast<int>(i % p.K);
-    const int64_t kw = k >> 3;
-    const uint32_t word = static_cast<uint32_t>(
-        (p.flags & QG_W4_LAYOUT_KN) ? p.w[kw * p.N + n] : p.w[static_cast<int64_t>(n) * (p.K >> 3) + kw]);
-    const int e = k & 7;
-    int u = static_cast<int>((word >> (high ? 28 - 4 * e : 4 * e)) & 15u);
-    if (sgn) u ^= 8;
-    const GroupParams gp = group_params(p, n, k / p.group, 0.0f);
-    const int cen = u - static_cast<int>(gp.zb);
-    if (p.out_dtype == QG_I8) {
-      static_cast<int8_t*>(p.out)[i] = static_cast<int8_t>(cen);
+  for (int qi = blockIdx.x * blockDim.x + threadIdx.x; qi < quads; qi += gridDim.x * blockDim.x) {
+    int n, kq;
+    if (kn) {
+      kq = qi / p.N;
+      n = qi - kq * p.N;
     } else {
-      const float v = static_cast<float>(cen) * gp.s;
-      store_out(p.out, p.out_dtype, i, v);
+      n = qi / KQ;
+      kq = qi - n * KQ;
     }
-    (void)ng;
+    const int kw0 = 4 * kq;
+    uint32_t word[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      word[j] = p.w[kn ? static_cast<int64_t>(kw0 + j) * p.N + n : static_cast<int64_t>(n) * KW + kw0 + j];
+    const GroupParams gp = group_params(p, n, (8 * kw0) / p.group, 0.0f);
+    const int zu = static_cast<int>(gp.zb);
+    const int64_t base = static_cast<int64_t>(n) * p.K + 8 * kw0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int cen[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        int u = static_cast<int>((word[j] >> (high ? 28 - 4 * e : 4 * e)) & 15u);
+        if (sgn) u ^= 8;
+        cen[e] = u - zu;
+      }
+      const int64_t o0 = base + 8 * j;
+      if constexpr (OUT == QG_I8) {
+        uint32_t b[2] = {0, 0};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[e >> 2] |= (static_cast<uint32_t>(cen[e]) & 0xffu) << (8 * (e & 3));
+        int8_t* o = static_cast<int8_t*>(p.out) + o0;
+        if (vec) *reinterpret_cast<uint2*>(o) = make_uint2(b[0], b[1]);
+        else for (int e = 0; e < 8; ++e) o[e] = static_cast<int8_t>(cen[e]);
+      } else if constexpr (OUT == QG_F32) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(cen[e]) * gp.s;
+        float* o = static_cast<float*>(p.out) + o0;
+        if (vec) {
+          reinterpret_cast<float4*>(o)[0] = make_float4(v[0], v[1], v[2], v[3]);
+          reinterpret_cast<float4*>(o)[1] = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+          for (int e = 0; e < 8; ++e) o[e] = v[e];
+        }
+      } else {
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const float a = static_cast<float>(cen[e]) * gp.s, b = static_cast<float>(cen[e + 1]) * gp.s;
+          const uint32_t ha = OUT == QG_F16 ? f32_to_f16(a) : f32_to_bf16(a);
+          const uint32_t hb = OUT == QG_F16 ? f32_to_f16(b) : f32_to_bf16(b);
+          h[e >> 1] = ha | (hb << 16);
+        }
+        uint16_t* o = static_cast<uint16_t*>(p.out) + o0;
+        if (vec) *reinterpret_cast<uint4*>(o) = make_uint4(h[0], h[1], h[2], h[3]);
+        else for (int e = 0; e < 8; ++e) o[e] = static_cast<uint16_t>(h[e >> 1] >> (16 * (e & 1)));
+      }
+    }
   }
 }
 
@@ -769,10 +817,19 @@ hipError_t launch_w4_pack(const W4PackArgs& p, hipStream_t stream) {
 }
 
 hipError_t launch_w4_unpack(const W4Args& p, hipStream_t stream) {
-  const int64_t total = static_cast<int64_t>(p.N) * p.K;
-  int64_t blocks = ceil_div<int64_t>(total, 256);
+  const int64_t quads = static_cast<int64_t>(p.N) * (p.K / 32);  // K % 32 == 0 (group multiple)
+  if (quads == 0) return hipSuccess;
+  int64_t blocks = ceil_div<int64_t>(quads, 256);
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(k_w4_unpack, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p);
+  const int es = p.out_dtype == QG_I8 ? 1 : p.out_dtype == QG_F32 ? 4 : 2;
+  const int vec = (reinterpret_cast<uintptr_t>(p.out) % (8 * es)) == 0 ? 1 : 0;  // rows of K % 32 == 0
+  const dim3 grid(static_cast<unsigned>(blocks));
+  switch (p.out_dtype) {
+    case QG_I8: hipLaunchKernelGGL(k_w4_unpack<QG_I8>, grid, dim3(256), 0, stream, p, vec); break;
+    case QG_F32: hipLaunchKernelGGL(k_w4_unpack<QG_F32>, grid, dim3(256), 0, stream, p, vec); break;
+    case QG_F16: hipLaunchKernelGGL(k_w4_unpack<QG_F16>, grid, dim3(256), 0, stream, p, vec); break;
+    default: hipLaunchKernelGGL(k_w4_unpack<QG_BF16>, grid, dim3(256), 0, stream, p, vec); break;
+  }
   return hipGetLastError();
 }
 

@@ -424,6 +424,42 @@ __global__ void k_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64
   }
 }
 
+// The same for unit K stride, 16-byte aligned rows and output: one thread per
+// 16 bytes (one 16-byte load, 16 outputs in 2- or 4-byte vector stores).
+template <int OUT>
+__global__ __launch_bounds__(256) void k_fp8_decode16(const uint8_t* w, int64_t w_sn, int n, int K, int e5,
+                                                      void* out) {
+  const int cpr = K >> 4;  // 16-byte chunks per row (< 2^27)
+  const int chunks = n * cpr;
+  for (int ci = blockIdx.x * blockDim.x + threadIdx.x; ci < chunks; ci += gridDim.x * blockDim.x) {
+    const int r = ci / cpr, c = ci - r * cpr;
+    const uint4 v = *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(r) * w_sn + 16 * c);
+    const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+    const int64_t o0 = static_cast<int64_t>(r) * K + 16 * c;
+    if constexpr (OUT == QG_F32) {
+      float* o = static_cast<float*>(out) + o0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        reinterpret_cast<float4*>(o)[q] =
+            make_float4(fp8_to_f32(wd[q] & 0xffu, e5), fp8_to_f32((wd[q] >> 8) & 0xffu, e5),
+                        fp8_to_f32((wd[q] >> 16) & 0xffu, e5), fp8_to_f32(wd[q] >> 24, e5));
+    } else {
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        const float a = fp8_to_f32((wd[e >> 2] >> (8 * (e & 3))) & 0xffu, e5);
+        const float b = fp8_to_f32((wd[e >> 2] >> (8 * ((e + 1) & 3))) & 0xffu, e5);
+        const uint32_t ha = OUT == QG_F16 ? f32_to_f16(a) : f32_to_bf16(a);
+        const uint32_t hb = OUT == QG_F16 ? f32_to_f16(b) : f32_to_bf16(b);
+        h[e >> 1] = ha | (hb << 16);
+      }
+      uint4* o = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + o0);
+      o[0] = make_uint4(h[0], h[1], h[2], h[3]);
+      o[1] = make_uint4(h[4], h[5], h[6], h[7]);
+    }
+  }
+}
+
 unsigned grid_for(int64_t total) {
   const int64_t blocks = ceil_div<int64_t>(total, 256);
   return static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
@@ -442,6 +478,20 @@ hipError_t launch_pack_rows_u16(const uint16_t* src, int64_t s_r, int64_t s_k, i
 hipError_t launch_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64_t n, int64_t K, int e5,
                              void* out, int out_dtype, hipStream_t stream) {
   if (n * K == 0) return hipSuccess;
+  const bool vec = w_sk == 1 && K % 16 == 0 && w_sn % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0 && n * K < (int64_t(1) << 31);
+  if (vec) {
+    const int64_t chunks = n * K / 16;
+    const unsigned grid = static_cast<unsigned>(chunks / 256 + 1 < 65536 ? chunks / 256 + 1 : 65536);
+    const int ni = static_cast<int>(n), ki = static_cast<int>(K);
+    if (out_dtype == QG_F32)
+      hipLaunchKernelGGL(k_fp8_decode16<QG_F32>, dim3(grid), dim3(256), 0, stream, w, w_sn, ni, ki, e5, out);
+    else if (out_dtype == QG_F16)
+      hipLaunchKernelGGL(k_fp8_decode16<QG_F16>, dim3(grid), dim3(256), 0, stream, w, w_sn, ni, ki, e5, out);
+    else
+      hipLaunchKernelGGL(k_fp8_decode16<QG_BF16>, dim3(grid), dim3(256), 0, stream, w, w_sn, ni, ki, e5, out);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(k_fp8_decode, dim3(grid_for(n * K)), dim3(256), 0, stream, w, w_sn, w_sk, n, K, e5, out,
                      out_dtype);
   return hipGetLastError();

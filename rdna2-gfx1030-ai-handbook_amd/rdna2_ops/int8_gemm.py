@@ -126,10 +126,12 @@ def _launch(a, b, a_scale, b_scale, bias, *, tile, num_warps, num_stages, group_
     _lib.check(status, "qg_int8_gemm")
     if not return_kernel:
         return out
+    # the C ABI's choice: >= 192 tiles of 256 x 192 take the persistent 8-wave
+    # ping-pong kernel, smaller grids the 4-wave 128 x 128 one (K stage 128)
     big = (-(-m // 256)) * (-(-n // 192)) >= 192
-    tile_used = (256, 192, 64) if big else (128, 128, 64)
-    meta = _lib.kernel_metadata("int8_mfma_16x16x64_lds_dma", tile_used,
-                                "k_i8_gemmILi256ELi192E" if big else "k_i8_gemmILi128ELi128E")
+    tile_used = (256, 192, 128) if big else (128, 128, 128)
+    meta = _lib.kernel_metadata("int8_mfma_32x32x32_pingpong" if big else "int8_mfma_32x32x32", tile_used,
+                                "k_i8_gemm_ppINS0_5I8GeoILi256ELi192E" if big else "k_i8_gemmINS0_5I8GeoILi128ELi128E")
     meta.update(packed_operands=ws_bytes > 0, requested_tile=list(tile), epilogue_flags=flags)
     return out, meta
 

@@ -229,3 +229,17 @@ def test_cfg3_full_size(cuda, n):
     y64 = o8.fp8_linear(av, codes, s)
     absdot = o8.fp8_linear(np.abs(av), codes & 0x7F, s)
     check(y[torch.from_numpy(rows).to(cuda)], y64, absdot, torch.bfloat16, f"cfg3 n{n}")
+
+
+def test_fused_metadata_names_the_launched_tile(cuda):
+    """The metadata of the fused method reports the tile the C ABI chose
+    (256 x 128 from four such tiles per CU) and that kernel's resources."""
+    for m, n, tile in ((128, 256, [128, 128, 128]), (1024, 32768, [256, 128, 128])):
+        case(f"fp8 metadata {m}x{n}")
+        a = torch.ones(m, 128, dtype=torch.bfloat16, device=cuda)
+        w = torch.ones(n, 128, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)  # 0x01: 2^-9
+        md = {}
+        y = mod().fp8_weight_gemm(a, w, method="fused_dot2", metadata=md)
+        assert float(y[0, 0]) == 128 * 2.0 ** -9
+        assert md["tile"] == [64, 64, 32]  # the requested tile, as the reference reports it
+        assert md["launched_tile"] == tile and md["vgpr"] is not None and md["spills"] == 0

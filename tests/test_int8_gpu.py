@@ -294,3 +294,20 @@ def test_cfg1_chain_stages(cuda, stage):
             print("bad", int(bad.sum()), "max", float(d.max()),
                   [(tuple(i), float(got[tuple(i)]), float(exp[tuple(i)])) for i in idx], flush=True)
         assert not bad.any()
+
+
+def test_int8_return_kernel_metadata(cuda):
+    """return_kernel names the kernel the C ABI launched (4-wave tile for small
+    grids, persistent ping-pong for >= 192 tiles of 256 x 192) with its
+    compiler-reported resources."""
+    from rdna2_ops.int8_gemm import int8_gemm_dequant
+    for m, n, variant, tile in ((64, 64, "int8_mfma_32x32x32", [128, 128, 128]),
+                                (4096, 3072, "int8_mfma_32x32x32_pingpong", [256, 192, 128])):
+        case(f"int8 metadata {m}x{n}")
+        a = torch.ones(m, 128, dtype=torch.int8, device=cuda)
+        w = torch.ones(n, 128, dtype=torch.int8, device=cuda)
+        out, md = int8_gemm_dequant(a, w.T, torch.ones(m, device=cuda), torch.ones(n, device=cuda),
+                                    return_kernel=True)
+        assert float(out[0, 0]) == 128.0
+        assert md["variant"] == variant and md["tile"] == tile
+        assert md["vgpr"] is not None and md["spills"] == 0 and md["scratch_bytes"] == 0

@@ -158,7 +158,11 @@ def test_int4_linear_a16_methods(cuda):
     y = mod.int4_linear_a16(a, p, bias=b, method="prepared", prepared=wp)
     assert np.abs(y.float().cpu().numpy() - ref_out).max() <= 1e-2 * rms
     y, md = mod.int4_linear_a16(a, p, bias=b, method="dot2", return_kernel=True)
-    assert md["variant"] == "w4a16_skinny"
+    assert md["variant"] == "w4a16_decode" and md["vgpr"] is not None  # 5 rows, K 256
+    y, md = mod.int4_linear_a16(torch.cat([a] * 8), p, bias=b, method="dot2", return_kernel=True)
+    assert md["variant"] == "w4a16_skinny" and md["vgpr"] is not None  # 40 rows
+    y, md = mod.int4_linear_a16(torch.cat([a] * 20), p, bias=b, method="dot2", return_kernel=True)
+    assert md["variant"] == "w4a16_tiled_mfma" and md["vgpr"] is not None  # 100 rows
     with pytest.raises(ValueError):
         mod.int4_linear_a16(a.float(), p)
     with pytest.raises(ValueError):

@@ -203,6 +203,24 @@ def run_w4a16(torch, lib, _lib, dev, copies=12):
         out[m] = {"us": round(ms * 1e3, 2), "GBs": round(bytes_ / (ms * 1e-3) / 1e9, 1),
                   "frac_hbm_peak": round(bytes_ / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                   "TFLOPs": round(2 * m * N * K / (ms * 1e-3) / 1e12, 1), "bytes": bytes_}
+        if m == 2048:
+            # the reference's default method at the same shape: this library's
+            # unpack to bf16, then the library (hipBLASLt) GEMM, HIP events over
+            # eager calls (the reference API is eager-only)
+            def dequant(a=a):
+                return w4.int4_linear_a16(a, p0, method="dequant")
+            for _ in range(3):
+                dequant()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                dequant()
+            e1.record()
+            torch.cuda.synchronize()
+            dms = e0.elapsed_time(e1) / 10
+            out["2048_dequant_method"] = {"us": round(dms * 1e3, 2),
+                                          "TFLOPs": round(2 * m * N * K / (dms * 1e-3) / 1e12, 1)}
     return out
 
 
@@ -389,6 +407,7 @@ def main():
         sec["w4a16_m1"] = w4[1]
         sec["w4a16_m16"] = w4[16]
         sec["w4a16_prefill_m2048"] = w4[2048]
+        sec["w4a16_prefill_m2048_dequant_method"] = w4["2048_dequant_method"]
         sec["fp8_cfg3"] = run_fp8(torch, lib, _lib, dev)
         sec["moe_cfg4"] = run_moe(torch, dev)
         sec["w4a8"] = run_w4a8(torch, dev)

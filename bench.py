@@ -243,6 +243,23 @@ def run_fp8(torch, lib, _lib, dev):
         ms = _graph_time(torch, call, 10, replays=2)
         tf = 2 * m * n * k / (ms * 1e-3) / 1e12
         res[n] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+        # the reference's decode method: this library's fp8 -> bf16 decode,
+        # then the library (hipBLASLt) GEMM, HIP events over eager calls;
+        # without the per-channel scale (the reference has none; with it the
+        # method adds fp32 passes over the output that the fused epilogue avoids)
+        def decode(a=a, codes=codes):
+            return f8.fp8_weight_gemm(a, codes, method="decode")
+        for _ in range(3):
+            decode()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            decode()
+        e1.record()
+        torch.cuda.synchronize()
+        dms = e0.elapsed_time(e1) / 10
+        res[f"{n}_decode_method_unscaled"] = {"us": round(dms * 1e3, 1), "TFLOPs": round(2 * m * n * k / (dms * 1e-3) / 1e12, 1)}
     return res
 
 

@@ -311,3 +311,35 @@ def test_int8_return_kernel_metadata(cuda):
         assert float(out[0, 0]) == 128.0
         assert md["variant"] == variant and md["tile"] == tile
         assert md["vgpr"] is not None and md["spills"] == 0 and md["scratch_bytes"] == 0
+
+
+def _sweep_shapes():
+    """Seeded ragged shapes on both sides of the kernel choice: below 192 tiles
+    of 256 x 192 (4-wave kernel), 192-256 (one tile per persistent workgroup)
+    and above 256 (several), with K not a multiple of 16 (packed operands)."""
+    rng = np.random.default_rng(20261202)
+    shapes = []
+    for lo_m, hi_m, lo_n, hi_n in ((33, 700, 17, 900), (2900, 4200, 2500, 3300), (4300, 6000, 3300, 6000)):
+        for _ in range(3):
+            shapes.append((int(rng.integers(lo_m, hi_m)), int(rng.integers(lo_n, hi_n)), int(rng.integers(1, 400))))
+    return shapes
+
+
+@pytest.mark.parametrize("m,n,k", _sweep_shapes())
+def test_int8_random_shape_sweep(cuda, m, n, k):
+    """int32 product and the order-F bf16 epilogue with bias, bit-exact against
+    the oracle, on the sweep's shape."""
+    from rdna2_ops.int8_gemm import int8_gemm_dequant, int8_matmul
+    case(f"int8 sweep {m}x{n}x{k}")
+    g = torch.Generator().manual_seed(m * 31 + n * 7 + k)
+    a = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    sa = torch.rand(m, generator=g) * 0.02 + 0.001
+    sb = torch.rand(n, generator=g) * 0.02 + 0.001
+    bias = torch.randn(n, generator=g).to(torch.bfloat16)
+    acc_o = o.int8_matmul(a.numpy(), np.ascontiguousarray(w.numpy().T))
+    ag, wg = a.to(cuda), w.to(cuda)
+    assert np.array_equal(int8_matmul(ag, wg.T).cpu().numpy(), acc_o)
+    got = int8_gemm_dequant(ag, wg.T, sa.to(cuda), sb.to(cuda), bias.to(cuda), out_dtype=torch.bfloat16)
+    ref = o.epilogue_f(acc_o, sa.numpy(), sb.numpy(), bias.float().numpy(), out="bf16")
+    assert np.array_equal(_bits(got, "bf16"), _bits(ref, "bf16"))

@@ -226,7 +226,9 @@ def run_w4a16(torch, lib, _lib, dev, copies=12):
 
 def run_fp8(torch, lib, _lib, dev):
     """e4m3 weights with per-channel absmax/448 scales,
-    bf16 activations M 4096, K 3072, N 3072 and 12288, bf16 out."""
+    bf16 activations M 4096, K 3072, N 3072 and 12288, bf16 out. Timed per
+    call of qg_fp8w_gemm: on these grids the exact fp8 -> bf16 decode of W into
+    the workspace plus the 2-byte ping-pong GEMM."""
     from rdna2_ops import fp8_weight_gemm_v06 as f8
     gen = torch.Generator().manual_seed(3)
     res = {}
@@ -236,10 +238,13 @@ def run_fp8(torch, lib, _lib, dev):
         a = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
         y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
         P = _lib.ptr
+        # workspace: the exactly decoded 2-byte weight on large grids
+        wsb = lib.qg_fp8w_gemm_workspace_bytes(P(a), k, 1, P(codes), k, 1, m, n, k)
+        ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=dev)
 
-        def call(i, stream, a=a, y=y, codes=codes, sc=sc, n=n):
+        def call(i, stream, a=a, y=y, codes=codes, sc=sc, n=n, ws=ws, wsb=wsb):
             _lib.check(lib.qg_fp8w_gemm(P(a), _lib.BF16, k, 1, m, k, P(codes), _lib.E4M3, k, 1, n, P(sc), None, 0,
-                                        P(y), _lib.BF16, None, 0, stream), "fp8w")
+                                        P(y), _lib.BF16, P(ws) if wsb else None, wsb, stream), "fp8w")
         ms = _graph_time(torch, call, 10, replays=2)
         tf = 2 * m * n * k / (ms * 1e-3) / 1e12
         res[n] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}

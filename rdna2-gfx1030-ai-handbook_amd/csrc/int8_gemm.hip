@@ -49,6 +49,30 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// The MFMA of the ping-pong main loop, W fragment first (transposed
+// accumulator): int8 32x32x32 -> int32, or 2-byte 32x32x16 -> fp32. Both take
+// a 16-byte fragment per lane (row l & 31, K chunk l >> 5 of the k-step), so
+// the ring layout, copies and fragment offsets are the same for both.
+struct MfmaI8 {
+  using acc_t = i32x16;
+  static __device__ __forceinline__ acc_t mfma(const i32x4& w, const i32x4& a, const acc_t& c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(w, a, c, 0, 0, 0);
+  }
+};
+template <bool F16>
+struct MfmaHalf {
+  using acc_t = f32x16;
+  static __device__ __forceinline__ acc_t mfma(const i32x4& w, const i32x4& a, const acc_t& c) {
+    if constexpr (F16)
+      return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, w), __builtin_bit_cast(f16x8, a), c,
+                                                    0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), __builtin_bit_cast(bf16x8, a),
+                                                     c, 0, 0, 0);
+  }
+};
 
 enum EpiMode { EPI_INT = 0, EPI_F = 1, EPI_FMA = 2, EPI_EAGER = 3, EPI_GELU = 4 };
 
@@ -117,11 +141,11 @@ constexpr int out_size() { return (OUT == QG_F16 || OUT == QG_BF16) ? 2 : 4; }
 //   EPI_FMA:   v = fma(f32(acc), sa * sb, bias)                 (rounding="fused", :191)
 //   EPI_EAGER: t = out(f32(acc) * (sa * sb)); t = out(t + out(bias))  (comfy_int8.py:128-143)
 //   EPI_GELU:  EPI_F followed by GELU-tanh in fp32
-template <int OUT, int MODE>
-__device__ __forceinline__ float epi_value(int32_t acc, float sa, float sb, float bv, bool has_bias) {
+template <int OUT, int MODE, typename ACC>
+__device__ __forceinline__ float epi_value(ACC acc, float sa, float sb, float bv, bool has_bias) {
 #pragma clang fp contract(off)
   const float scale = sa * sb;
-  const float accf = static_cast<float>(acc);
+  const float accf = static_cast<float>(acc);  // exact for int32 |acc| < 2^24, identity for fp32
   float v;
   if constexpr (MODE == EPI_EAGER) {
     v = round_to<OUT>(accf * scale);
@@ -219,10 +243,10 @@ template <int BM, int BN, int MODE>
 __device__ __forceinline__ EpiParams fetch_epi_params(const I8GemmArgs& p, int m0, int n0, int tid) {
   EpiParams e;
   if constexpr (MODE != EPI_INT) {
-    if (tid < BM) e.sa = p.a_scale[min(m0 + tid, p.M - 1)];
+    if (tid < BM) e.sa = p.a_scale ? p.a_scale[min(m0 + tid, p.M - 1)] : 1.0f;
     if (tid < BN) {
       const int col = min(n0 + tid, p.N - 1);
-      e.sb = p.b_scale[p.b_scalar ? 0 : col];
+      e.sb = p.b_scale ? p.b_scale[p.b_scalar ? 0 : col] : 1.0f;
       if (p.bias != nullptr) e.bias = load_bias_bits(p.bias, p.bias_dtype, col);
     }
   }
@@ -510,8 +534,8 @@ constexpr int pp_copies() { return (G::BM > G::BN ? G::BM : G::BN) / 32; }
 // return no copy is in flight and every wave has passed the barrier after the
 // last read of the rings, so each wave may stage its epilogue in its own part
 // of the rings at once (group X's epilogue overlaps group Y's last MFMAs).
-template <typename G, typename Park>
-__device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* smem, const char* a_base,
+template <typename G, typename MF, typename Park>
+__device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::FN], char* smem, const char* a_base,
                                             const char* w_base, const uint32_t (&voff)[pp_copies<G>()], int S,
                                             int wave, int lane, bool pre, Park&& park) {
   static_assert(G::NW == 8 && G::NA == 3 && G::KT == 4, "ping-pong geometry");
@@ -565,7 +589,7 @@ __device__ __forceinline__ void pp_mainloop(i32x16 (&acc)[G::FM][G::FN], char* s
     static_for<0, G::KT>([&](auto t) {
       static_for<0, G::FM>([&](auto i) {
         static_for<0, G::FN>([&](auto j) {
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[t][j], fa[t][i], acc[i][j], 0, 0, 0);
+          acc[i][j] = MF::mfma(fb[t][j], fa[t][i], acc[i][j]);
         });
       });
     });
@@ -659,8 +683,8 @@ __device__ __forceinline__ f32x4 col4(const float* v, int c0) { return *reinterp
 // column scales and fp32 bias values parked at SC_A, SC_B and SC_BIAS).
 // Full tiles are staged per wave in its own part of the rings and leave as
 // whole 16-byte row chunks; edge tiles store element-wise.
-template <typename G, int OUT, int MODE, int STAGE_BASE = 0, int REGION = G::RING / G::NW>
-__device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const i32x16 (&acc)[G::FM][G::FN], char* smem,
+template <typename G, int OUT, int MODE, int STAGE_BASE = 0, int REGION = G::RING / G::NW, typename ACCV = i32x16>
+__device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&acc)[G::FM][G::FN], char* smem,
                                             int m0, int n0, int wr, int wc, int wave, int lane) {
 #pragma clang fp contract(off)
   const float* sa_lds = reinterpret_cast<const float*>(smem + G::SC_A);
@@ -770,8 +794,11 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const i32x16 (&
 // epilogue, which stages in A slots 1-2, so the next tile's first copy latency
 // overlaps the epilogue; a barrier after the epilogue keeps the next tile's
 // parked parameters and stage-1 copies off the LDS the epilogue still reads.
-template <typename G, int OUT, int MODE>
-__global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
+// The body is shared by the INT8 kernel (MF = MfmaI8, 1-byte operands) and the
+// 2-byte kernel (MfmaHalf, fp16 / bf16 operands: a 128-byte stage row holds 64
+// K elements, four 32x32x16 k-steps); ES is the operand element size.
+template <typename G, int OUT, int MODE, typename MF, int ES>
+__device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
 #pragma clang fp contract(off)
   constexpr int YS = pp_copies<G>();
   constexpr bool PREF = out_size<OUT>() == 2;
@@ -785,7 +812,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
   const int wr = wave / G::WGN, wc = wave % G::WGN;
   const bool grp_x = wave < 4;
   const int total = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
-  const int S = p.K / G::KS;
+  const int S = p.K * ES / G::KS;
   const char* a_base = reinterpret_cast<const char*>(p.a);
   const char* w_base = reinterpret_cast<const char*>(p.w);
 
@@ -796,7 +823,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
   auto plan_offsets = [&](int m0_, int n0_) __attribute__((always_inline)) {
     const CopyPlan<4> plan(grp_x ? n0_ : m0_, wave & 3, lane);
     const int rows = grp_x ? p.N : p.M;
-    const uint32_t stride = static_cast<uint32_t>(grp_x ? p.w_sn : p.a_sm);
+    const uint32_t stride = static_cast<uint32_t>((grp_x ? p.w_sn : p.a_sm) * ES);  // bytes
     static_for<0, YS>([&](auto i_c) {
       constexpr int I = decltype(i_c)::value;
       voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, rows - 1)) * stride + plan.chunk16;
@@ -809,7 +836,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
   EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
   plan_offsets(m0, n0);
   bool pre = false;
-  i32x16 acc[G::FM][G::FN];
+  typename MF::acc_t acc[G::FM][G::FN];
   for (;;) {
     // The lane index passes through an opaque copy per tile: lane-derived LDS
     // and global offsets of the main loop and the epilogue are then recomputed
@@ -818,7 +845,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
     int lane_t = lane;
     asm volatile("" : "+v"(lane_t));
     static_for<0, G::FM>([&](auto i) {
-      static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
+      static_for<0, G::FN>([&](auto j) { acc[i][j] = typename MF::acc_t{}; });
     });
     auto park = [&]() __attribute__((always_inline)) {
       if constexpr (MODE != EPI_INT) {
@@ -829,7 +856,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
         }
       }
     };
-    pp_mainloop<G>(acc, smem, a_base, w_base, voff, S, wave, lane_t, pre, park);
+    pp_mainloop<G, MF>(acc, smem, a_base, w_base, voff, S, wave, lane_t, pre, park);
     const int tn = t + static_cast<int>(gridDim.x);
     const bool more = tn < total;
     int m1 = 0, n1 = 0;
@@ -849,6 +876,20 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
     ep = ep1;
     pre = PREF && S > 0;
   }
+}
+
+template <typename G, int OUT, int MODE>
+__global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
+  pp_gemm_body<G, OUT, MODE, MfmaI8, 1>(p);
+}
+
+// fp16 / bf16 A [M, K] and W [N, K] (K a multiple of 64, 16-byte aligned
+// rows): out = f32(acc) * (1 * w_scale[n]) + bias in order F, one rounding.
+// Serves the fp8 weight-only GEMM on large grids, after an exact fp8 -> 2-byte
+// decode of W.
+template <typename G, int OUT, bool F16A>
+__global__ __launch_bounds__(G::THREADS, 1) void k_h16_gemm_pp(I8GemmArgs p) {
+  pp_gemm_body<G, OUT, EPI_F, MfmaHalf<F16A>, 2>(p);
 }
 
 __device__ __forceinline__ float silu(float g) {
@@ -945,7 +986,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
     }
     if (tid < G::BN) sb_lds[tid] = ld_sb;
   };
-  pp_mainloop<G>(acc, smem, reinterpret_cast<const char*>(p.a),
+  pp_mainloop<G, MfmaI8>(acc, smem, reinterpret_cast<const char*>(p.a),
                  reinterpret_cast<const char*>(p.w) + static_cast<int64_t>(e) * p.w_estride, voff, p.K / G::KS,
                  wave, lane, false, park);
 
@@ -1129,6 +1170,23 @@ hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream) {
   const long big = static_cast<long>(ceil_div(p.M, 256)) * ceil_div(p.N, 192);
   if (big >= 192) return launch_variant<I8Geo<256, 192, 4, 2, 3>, 1>(p, stream);
   return launch_variant<I8Geo<128, 128, 2, 2, 2>, 2>(p, stream);
+}
+
+hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream) {
+  using G = I8Geo<256, 192, 4, 2, 3>;
+  const int tiles = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
+  if (tiles == 0) return hipSuccess;
+  const dim3 grid(tiles < kPersistentCUs ? tiles : kPersistentCUs);
+#define QG_H16(OUT)                                                                                   \
+  do {                                                                                                \
+    if (f16a) hipLaunchKernelGGL((k_h16_gemm_pp<G, OUT, true>), grid, dim3(G::THREADS), 0, stream, p); \
+    else hipLaunchKernelGGL((k_h16_gemm_pp<G, OUT, false>), grid, dim3(G::THREADS), 0, stream, p);    \
+  } while (0)
+  if (p.out_dtype == QG_F16) QG_H16(QG_F16);
+  else if (p.out_dtype == QG_BF16) QG_H16(QG_BF16);
+  else QG_H16(QG_F32);
+#undef QG_H16
+  return hipGetLastError();
 }
 
 }  // namespace qg

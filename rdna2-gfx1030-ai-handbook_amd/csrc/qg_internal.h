@@ -41,6 +41,9 @@ struct I8GemmArgs {
 
 hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream);
 hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream);
+// 2-byte (fp16 / bf16) A and W on the ping-pong main loop; p.a_sm / p.w_sn /
+// p.K in elements, a_scale null (1), b_scale per column or null (1).
+hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream);
 
 // MoE routing and dispatch: see include/qgemm.h (qg_moe_dispatch).
 struct MoeDispatchArgs {

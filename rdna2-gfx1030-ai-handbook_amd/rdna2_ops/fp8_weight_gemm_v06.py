@@ -177,12 +177,19 @@ def fp8_weight_gemm(a, w, *, bias=None, method="upcast", prepared=None, tile=(64
         raise ValueError("Unsupported tile or warp count")
     result = _fused(a, w, bias, w_scale)
     if metadata is not None:
-        # the C ABI's choice: 256 x 128 tiles from four of them per CU
+        # the C ABI's choice: >= 192 tiles of 256 x 192 decode W exactly to A's
+        # type and run the 2-byte ping-pong GEMM; smaller grids the fused
+        # decode kernel (256 x 128 tiles from four of them per CU)
         m, n = a.shape[0], w.shape[0]
-        wide = m >= 256 and (-(-m // 256)) * (-(-n // 128)) >= 4 * 256
-        tile_used = (256, 128, 128) if wide else (128, 128, 128)
-        hint = "k_wd_gemmILi{}ELi128ELb0ELb{}ELi2ELi4ELi{}ELi128E".format(
-            3 if w.dtype == torch.float8_e5m2 else 2, int(a.dtype == torch.float16), tile_used[0])
-        metadata.update(_lib.kernel_metadata("fp8_fused_mfma", tile_used, hint), method=method,
+        f16 = int(a.dtype == torch.float16)
+        if (-(-m // 256)) * (-(-n // 192)) >= 192:
+            variant, tile_used = "fp8_decode_bf16_pingpong", (256, 192, 64)
+            hint = "k_h16_gemm_ppINS0_5I8GeoILi256ELi192E"
+        else:
+            wide = m >= 256 and (-(-m // 256)) * (-(-n // 128)) >= 4 * 256
+            variant, tile_used = "fp8_fused_mfma", ((256, 128, 128) if wide else (128, 128, 128))
+            hint = "k_wd_gemmILi{}ELi128ELb0ELb{}ELi2ELi4ELi{}ELi128E".format(
+                3 if w.dtype == torch.float8_e5m2 else 2, f16, tile_used[0])
+        metadata.update(_lib.kernel_metadata(variant, tile_used, hint), method=method,
                         tile=list(tile), launched_tile=list(tile_used), num_warps=num_warps)
     return result

@@ -232,9 +232,10 @@ def test_cfg3_full_size(cuda, n):
 
 
 def test_fused_metadata_names_the_launched_tile(cuda):
-    """The metadata of the fused method reports the tile the C ABI chose
-    (256 x 128 from four such tiles per CU) and that kernel's resources."""
-    for m, n, tile in ((128, 256, [128, 128, 128]), (1024, 32768, [256, 128, 128])):
+    """The metadata of the fused method reports the kernel and tile the C ABI
+    chose (decode + 2-byte ping-pong GEMM from 192 tiles of 256 x 192) and
+    that kernel's resources."""
+    for m, n, tile in ((128, 256, [128, 128, 128]), (1024, 32768, [256, 192, 64])):
         case(f"fp8 metadata {m}x{n}")
         a = torch.ones(m, 128, dtype=torch.bfloat16, device=cuda)
         w = torch.ones(n, 128, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)  # 0x01: 2^-9

@@ -450,15 +450,17 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
     return KN ? 4u * (static_cast<uint32_t>(kw) * p.N + n) : 4u * (static_cast<uint32_t>(n) * KW + kw);
   };
 
-  // ---- 1. this wave's activation slice (issued first: it is needed first) --
-  i32x4 av[RP];
-  {
-    const int k = min(c0 * 128 + 8 * lane, p.K - 8);
+  // ---- 1. this wave's activation slice (issued first: it is needed first):
+  // CH 128-wide chunks = CH / 4 16-byte loads per lane and row
+  constexpr int AV = CH / 4;
+  i32x4 av[RP][AV];
+  static_for<0, AV>([&](auto h) {
+    const int k = min(c0 * 128 + 512 * h + 8 * lane, p.K - 8);
     static_for<0, RP>([&](auto r) {
       const uint32_t roff = 2u * static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.a_sm);
-      av[r] = load_at<i32x4>(p.a, roff + 2u * k);
+      av[r][h] = load_at<i32x4>(p.a, roff + 2u * k);
     });
-  }
+  });
 
   // ---- 2. every weight / scale / zero load of this wave, in chunk order ----
   // UINT4 (group 128: chunk c is group c; launcher: CH chunks per wave and
@@ -508,7 +510,11 @@ __global__ __launch_bounds__(64 * WAVES) void k_w4_decode(W4Args p) {
 
   // ---- 3. activations -> this wave's LDS rows, even/odd order --------------
   char* const abase = smem + wave * RP * ROWB;
-  static_for<0, RP>([&](auto r) { *reinterpret_cast<i32x4*>(abase + r * ROWB + 16 * lane) = even_odd(av[r]); });
+  static_for<0, RP>([&](auto r) {
+    static_for<0, AV>([&](auto h) {
+      *reinterpret_cast<i32x4*>(abase + r * ROWB + 1024 * h + 16 * lane) = even_odd(av[r][h]);
+    });
+  });
 
   f32x4 total[CT], acc[CT], asum;
   static_for<0, CT>([&](auto t) { total[t] = f32x4{0, 0, 0, 0}; });

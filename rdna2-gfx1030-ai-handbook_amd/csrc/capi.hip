@@ -534,7 +534,7 @@ extern "C" int qg_fp8w_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_
     // every finite fp8 value is exact in fp16 and bf16: decode W once, then the
     // 2-byte ping-pong GEMM (same fp32 products, order-F epilogue)
     uint16_t* wd = reinterpret_cast<uint16_t*>(ws + pl.a_bytes + pl.w_bytes);
-    hipError_t e = qg::launch_fp8_decode(p.w8, p.w8_sn, 1, n, pl.kp, p.fp8_e5, wd, a_dtype, s);
+    hipError_t e = qg::launch_fp8_expand(p.w8, p.w8_sn, n, pl.kp, p.fp8_e5, wd, p.a_f16 != 0, s);
     if (e != hipSuccess) return e;
     qg::I8GemmArgs g{};
     g.a = reinterpret_cast<const int8_t*>(p.a);

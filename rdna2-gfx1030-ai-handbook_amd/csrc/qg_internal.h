@@ -161,6 +161,10 @@ hipError_t launch_pack_rows_u16(const uint16_t* src, int64_t s_r, int64_t s_k, i
                                 uint16_t* dst, int64_t k_pad, hipStream_t stream);
 hipError_t launch_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64_t n, int64_t K, int e5,
                              void* out, int out_dtype, hipStream_t stream);
+// fp8 -> fp16 / bf16 weight with the hardware conversion (exact for finite
+// values; element-wise decode when rows are not 16-byte aligned).
+hipError_t launch_fp8_expand(const uint8_t* w, int64_t w_sn, int64_t n, int64_t K, int e5, void* out, bool f16,
+                             hipStream_t stream);
 hipError_t launch_wd_fp8(const WdArgs& p, hipStream_t stream);
 
 hipError_t launch_w4a16(const W4Args& p, hipStream_t stream);

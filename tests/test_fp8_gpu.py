@@ -86,6 +86,27 @@ def test_fused_conversion_all_patterns(cuda, e5, adtype):
     assert np.array_equal(got, ref.astype(np.float32))
 
 
+@pytest.mark.parametrize("e5", [False, True])
+@pytest.mark.parametrize("adtype", [torch.bfloat16, torch.float16])
+def test_decode_path_conversion_all_patterns(cuda, e5, adtype):
+    """Large grids (>= 192 tiles of 256 x 192) expand the weight into the
+    workspace and run the 2-byte ping-pong GEMM: one-hot activation rows read
+    every finite code of every column back exactly."""
+    case(f"fp8 decode path all patterns e5={e5} {adtype}")
+    codes = np.arange(256, dtype=np.uint8)
+    vals = o8.decode_bits(codes, e5)
+    codes = codes[np.isfinite(vals)]
+    m, n, k = 1024, 9216, 128
+    wmat = codes[(np.arange(n)[:, None] + np.arange(k)[None, :]) % len(codes)].astype(np.uint8)
+    a = torch.zeros(m, k, dtype=adtype)
+    a[torch.arange(m), torch.arange(m) % k] = 1
+    md = {}
+    y = mod().fp8_weight_gemm(a.to(cuda), codes_tensor(wmat, e5, cuda), method="fused_dot2", metadata=md)
+    assert md["launched_tile"] == [256, 192, 64]  # the decode + ping-pong path
+    ref = o8.decode_bits(wmat, e5)[:, np.arange(m) % k].T  # out[m, n] = w[n, m % k]
+    assert np.array_equal(y.float().cpu().numpy(), ref.astype(np.float32))
+
+
 def _case(cuda, m, n, k, e5, adtype, scaled, bias, seed, a_pad=0, w_view=False):
     rng = np.random.default_rng(seed)
     wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)

@@ -36,6 +36,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);
 }
+// Two fp32 -> packed bf16 (a in the low half) with gfx950's v_cvt_pk_bf16_f32:
+// round-to-nearest-even, the bits of f32_to_bf16 for every non-NaN input.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+  typedef __bf16 bf16v2 __attribute__((ext_vector_type(2)));
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16v2));
+}
 // fp32 -> fp16, hardware conversion (round-to-nearest-even, fp16 denormals kept).
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));

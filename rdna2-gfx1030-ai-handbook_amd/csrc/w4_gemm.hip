@@ -668,6 +668,49 @@ __global__ void k_w4_pack(W4PackArgs p) {
 // outputs leave as 8- to 32-byte stores (element stores when `vec` is 0, an
 // output base that does not allow them). Threads walk the quads in storage
 // order (n fastest for the kn layout), so word loads are coalesced.
+// One packed word: 8 K values of a column, centred (u - zero point) and, for
+// floating outputs, scaled (exact fp32 product, one rounding to the output).
+template <int OUT>
+__device__ __forceinline__ void unpack_word_store(uint32_t word, bool high, bool sgn, int zu, float s, void* out,
+                                                  int64_t o0, int vec) {
+  if (sgn) word ^= 0x88888888u;  // q & 15 with q in [-8, 7] -> u = q + 8
+  int cen[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) cen[e] = static_cast<int>((word >> (high ? 28 - 4 * e : 4 * e)) & 15u) - zu;
+  if constexpr (OUT == QG_I8) {
+    uint32_t b[2] = {0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b[e >> 2] |= (static_cast<uint32_t>(cen[e]) & 0xffu) << (8 * (e & 3));
+    int8_t* o = static_cast<int8_t*>(out) + o0;
+    if (vec) *reinterpret_cast<uint2*>(o) = make_uint2(b[0], b[1]);
+    else for (int e = 0; e < 8; ++e) o[e] = static_cast<int8_t>(cen[e]);
+  } else if constexpr (OUT == QG_F32) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(cen[e]) * s;
+    float* o = static_cast<float*>(out) + o0;
+    if (vec) {
+      reinterpret_cast<float4*>(o)[0] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4*>(o)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+      for (int e = 0; e < 8; ++e) o[e] = v[e];
+    }
+  } else {
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float a = static_cast<float>(cen[e]) * s, b = static_cast<float>(cen[e + 1]) * s;
+      if constexpr (OUT == QG_F16) h[e >> 1] = f32_to_f16(a) | (static_cast<uint32_t>(f32_to_f16(b)) << 16);
+      else h[e >> 1] = f32x2_to_bf16x2(a, b);
+    }
+    uint16_t* o = static_cast<uint16_t*>(out) + o0;
+    if (vec) *reinterpret_cast<uint4*>(o) = make_uint4(h[0], h[1], h[2], h[3]);
+    else for (int e = 0; e < 8; ++e) o[e] = static_cast<uint16_t>(h[e >> 1] >> (16 * (e & 1)));
+  }
+}
+
+// kn layout: one thread per 4 packed words of a column (32 consecutive K, one
+// group lookup), 64 contiguous output bytes per thread.
 template <int OUT>
 __global__ __launch_bounds__(256) void k_w4_unpack(W4Args p, int vec) {
   const int KW = p.K >> 3, KQ = KW >> 2;  // words and word quads per column
@@ -690,48 +733,44 @@ __global__ __launch_bounds__(256) void k_w4_unpack(W4Args p, int vec) {
     for (int j = 0; j < 4; ++j)
       word[j] = p.w[kn ? static_cast<int64_t>(kw0 + j) * p.N + n : static_cast<int64_t>(n) * KW + kw0 + j];
     const GroupParams gp = group_params(p, n, (8 * kw0) / p.group, 0.0f);
-    const int zu = static_cast<int>(gp.zb);
     const int64_t base = static_cast<int64_t>(n) * p.K + 8 * kw0;
 #pragma unroll
+    for (int j = 0; j < 4; ++j)
+      unpack_word_store<OUT>(word[j], high, sgn, static_cast<int>(gp.zb), gp.s, p.out, base + 8 * j, vec);
+  }
+}
+
+// nk layout: a wave takes 256 consecutive packed words and lane l words
+// base + 64 j + l (j < 4), so each load (4 bytes per lane) and each store (8
+// values per lane) of the wave is contiguous, with four loads in flight per
+// lane. Word i of the weight holds K values [8 i, 8 i + 8) of the output's flat
+// [N, K] order; its group's scale and zero point come from the small scale /
+// zero arrays (cache hits).
+template <int OUT>
+__global__ __launch_bounds__(256) void k_w4_unpack_nk(W4Args p, int vec) {
+  const int KW = p.K >> 3;
+  const int words = p.N * KW;  // < 2^28 (N K < 2^31)
+  const bool sgn = p.flags & QG_W4_SIGNED_NIBBLES;
+  const bool high = p.flags & QG_W4_ORDER_HIGH;
+  const int lane = threadIdx.x & 63;
+  for (int base = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 256; base < words; base += gridDim.x * 1024) {
+    const int w0 = base + lane;
+    uint32_t word[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) word[j] = p.w[min(w0 + 64 * j, words - 1)];
+    int n = w0 / KW, kw = w0 - n * KW;
+#pragma unroll
     for (int j = 0; j < 4; ++j) {
-      int cen[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        int u = static_cast<int>((word[j] >> (high ? 28 - 4 * e : 4 * e)) & 15u);
-        if (sgn) u ^= 8;
-        cen[e] = u - zu;
+      const int wi = w0 + 64 * j;
+      if (wi < words) {
+        const GroupParams gp = group_params(p, n, (8 * kw) / p.group, 0.0f);
+        unpack_word_store<OUT>(word[j], high, sgn, static_cast<int>(gp.zb), gp.s, p.out, 8 * static_cast<int64_t>(wi),
+                               vec);
       }
-      const int64_t o0 = base + 8 * j;
-      if constexpr (OUT == QG_I8) {
-        uint32_t b[2] = {0, 0};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) b[e >> 2] |= (static_cast<uint32_t>(cen[e]) & 0xffu) << (8 * (e & 3));
-        int8_t* o = static_cast<int8_t*>(p.out) + o0;
-        if (vec) *reinterpret_cast<uint2*>(o) = make_uint2(b[0], b[1]);
-        else for (int e = 0; e < 8; ++e) o[e] = static_cast<int8_t>(cen[e]);
-      } else if constexpr (OUT == QG_F32) {
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(cen[e]) * gp.s;
-        float* o = static_cast<float*>(p.out) + o0;
-        if (vec) {
-          reinterpret_cast<float4*>(o)[0] = make_float4(v[0], v[1], v[2], v[3]);
-          reinterpret_cast<float4*>(o)[1] = make_float4(v[4], v[5], v[6], v[7]);
-        } else {
-          for (int e = 0; e < 8; ++e) o[e] = v[e];
-        }
-      } else {
-        uint32_t h[4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const float a = static_cast<float>(cen[e]) * gp.s, b = static_cast<float>(cen[e + 1]) * gp.s;
-          const uint32_t ha = OUT == QG_F16 ? f32_to_f16(a) : f32_to_bf16(a);
-          const uint32_t hb = OUT == QG_F16 ? f32_to_f16(b) : f32_to_bf16(b);
-          h[e >> 1] = ha | (hb << 16);
-        }
-        uint16_t* o = static_cast<uint16_t*>(p.out) + o0;
-        if (vec) *reinterpret_cast<uint4*>(o) = make_uint4(h[0], h[1], h[2], h[3]);
-        else for (int e = 0; e < 8; ++e) o[e] = static_cast<uint16_t>(h[e >> 1] >> (16 * (e & 1)));
+      kw += 64;
+      while (kw >= KW) {
+        kw -= KW;
+        ++n;
       }
     }
   }
@@ -830,6 +869,17 @@ hipError_t launch_w4_unpack(const W4Args& p, hipStream_t stream) {
   const int es = p.out_dtype == QG_I8 ? 1 : p.out_dtype == QG_F32 ? 4 : 2;
   const int vec = (reinterpret_cast<uintptr_t>(p.out) % (8 * es)) == 0 ? 1 : 0;  // rows of K % 32 == 0
   const dim3 grid(static_cast<unsigned>(blocks));
+  if (!(p.flags & QG_W4_LAYOUT_KN)) {
+    int64_t wblocks = ceil_div<int64_t>(quads * 4, 1024);  // 256 words per wave, 4 waves
+    const dim3 wgrid(static_cast<unsigned>(wblocks < 65536 ? wblocks : 65536));
+    switch (p.out_dtype) {
+      case QG_I8: hipLaunchKernelGGL(k_w4_unpack_nk<QG_I8>, wgrid, dim3(256), 0, stream, p, vec); break;
+      case QG_F32: hipLaunchKernelGGL(k_w4_unpack_nk<QG_F32>, wgrid, dim3(256), 0, stream, p, vec); break;
+      case QG_F16: hipLaunchKernelGGL(k_w4_unpack_nk<QG_F16>, wgrid, dim3(256), 0, stream, p, vec); break;
+      default: hipLaunchKernelGGL(k_w4_unpack_nk<QG_BF16>, wgrid, dim3(256), 0, stream, p, vec); break;
+    }
+    return hipGetLastError();
+  }
   switch (p.out_dtype) {
     case QG_I8: hipLaunchKernelGGL(k_w4_unpack<QG_I8>, grid, dim3(256), 0, stream, p, vec); break;
     case QG_F32: hipLaunchKernelGGL(k_w4_unpack<QG_F32>, grid, dim3(256), 0, stream, p, vec); break;

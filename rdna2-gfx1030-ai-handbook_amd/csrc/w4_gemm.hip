@@ -837,10 +837,12 @@ template <bool F16A>
 hipError_t launch_skinny(const W4Args& p, hipStream_t stream) {
   const int C = ceil_div(p.K, 128);
   if (p.M <= 16 && ceil_div(C, 8) <= kDecodeChunks) {
-    // one activation row: two column tiles per wave keep twice the waves in
-    // flight; 4 or 16 rows: four tiles share each activation fragment
+    // column tiles of 16 per workgroup, all sharing each activation fragment:
+    // two for 1-4 rows (cfg2, 448 workgroups: 2-4 rows 9.5-9.7 us against
+    // 10.0-10.1 us with four), four for 5-16 rows (11.2-11.4 us against 12.9 us
+    // with two)
     if (p.M == 1) return launch_decode_g<1, 2, F16A>(p, stream);
-    if (p.M <= 4) return launch_decode_g<4, 4, F16A>(p, stream);
+    if (p.M <= 4) return launch_decode_g<4, 2, F16A>(p, stream);
     return launch_decode_g<16, 4, F16A>(p, stream);
   }
   if (p.M <= 16) return launch_skinny_g<1, 4, F16A>(p, stream);

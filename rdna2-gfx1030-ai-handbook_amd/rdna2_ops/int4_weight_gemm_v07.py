@@ -303,7 +303,8 @@ def int4_linear_a16(a, p, *, bias=None, method="dequant", prepared=None, tile=(6
             return out, _lib.kernel_metadata("w4a16_tiled_mfma", (128, 128, 128), "k_wd_gemm")
         if m <= 16 and -(-p.k // 128) <= 32:
             rp = 1 if m == 1 else 4 if m <= 4 else 16
-            return out, _lib.kernel_metadata("w4a16_decode", (rp, 32, 128), "k_w4_decodeILi{}E".format(rp))
+            cols = 64 if rp == 16 else 32
+            return out, _lib.kernel_metadata("w4a16_decode", (rp, cols, 128), "k_w4_decodeILi{}E".format(rp))
         fm = 1 if m <= 16 else 2 if m <= 32 else 4
         return out, _lib.kernel_metadata("w4a16_skinny", (16 * fm, 16, 128), "k_w4_skinnyILi{}E".format(fm))
     return out

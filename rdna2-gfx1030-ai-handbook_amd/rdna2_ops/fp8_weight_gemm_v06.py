@@ -182,8 +182,10 @@ def fp8_weight_gemm(a, w, *, bias=None, method="upcast", prepared=None, tile=(64
         # decode kernel (256 x 128 tiles from four of them per CU)
         m, n = a.shape[0], w.shape[0]
         f16 = int(a.dtype == torch.float16)
-        if (-(-m // 256)) * (-(-n // 192)) >= 192:
-            variant, tile_used = "fp8_decode_bf16_pingpong", (256, 192, 64)
+        kp = -(-a.shape[1] // 128) * 128
+        if (-(-m // 256)) * (-(-n // 192)) >= 192 and 2 * max(m, n) * kp < 2 ** 31:
+            variant = "fp8_decode_f16_pingpong" if f16 else "fp8_decode_bf16_pingpong"
+            tile_used = (256, 192, 64)
             hint = "k_h16_gemm_ppINS0_5I8GeoILi256ELi192E"
         else:
             wide = m >= 256 and (-(-m // 256)) * (-(-n // 128)) >= 4 * 256

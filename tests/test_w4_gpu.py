@@ -67,6 +67,9 @@ def test_pack_unpack_reference_format(cuda, g, sym, layout, order):
     f32 = o4.unpack_int4_ref(r)
     assert np.array_equal(_np(w4().unpack_int4(p, dtype=torch.float32)), f32)
     assert np.array_equal(_np(w4().unpack_int4(p, dtype=torch.float16)), f32.astype(np.float16))
+    # bf16: torch's CPU round-to-nearest-even of the exact fp32 values, bit for bit
+    bf = torch.from_numpy(f32).to(torch.bfloat16).view(torch.int16)
+    assert torch.equal(w4().unpack_int4(p, dtype=torch.bfloat16).cpu().view(torch.int16), bf)
 
 
 @pytest.mark.parametrize("wdtype", [torch.float32, torch.float16, torch.bfloat16])

@@ -19,13 +19,23 @@ around each GEMM launch on its stream inside the timed steps.
 ``roofline_w4a16_decode`` is the metric's second half: the W4A16 decode kernel
 (M = 1) in GB/s against the 8 TB/s HBM peak, timed
 with events around graph replays of 120 launches over 12 rotated weight copies.
-``secondary`` holds cfg0, W4A16 M = 16 / 2048 and the FP8 configuration 3.
+``roofline_cfg0`` is the INT8 GEMM alone at BASELINE configuration 0, where
+the metric's >= 60 % bar is quoted. ``secondary`` holds cfg0's quantizer,
+W4A16 M = 16 / 2048, the FP8 configuration 3, MoE (configuration 4) and W4A8.
+
+Timing protocol (the reference's, rdna2-ops/bench_int8_gemm.py:259-268):
+--rounds alternating rounds (forward order on even rounds, reverse on odd) of
+the chain (exactly --steps steps per round between synchronisations), the
+cfg0 GEMM and quantizer and the two decode shapes; every figure is the median
+over rounds, the per-round samples are reported. ``clock`` is the GPU's GFX
+clock sampled with amdsmi during those rounds.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import statistics
 import sys
 from pathlib import Path
 
@@ -50,7 +60,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=("w4a16", "fp8", "moe", "w4a8"), default=None,
+    ap.add_argument("--rounds", type=int, default=3,
+                    help="alternating timing rounds; every figure is the median over rounds")
+    ap.add_argument("--only", choices=("w4a16", "fp8", "moe", "w4a8", "cfg0", "decode"), default=None,
                     help="run one secondary measurement alone and print it (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -108,48 +120,64 @@ class Chain:
                 events.append((i, e0, e1))
 
 
-def run_cfg0(torch, lib, _lib, quantize, synthetic, dev, iters=50):
-    """Secondary: cfg0 W8A8 linear (quant + GEMM) and the GEMM alone."""
-    c = synthetic.cfg0()
-    x, bias = c.x.to(dev), c.bias.to(dev)
-    wq, ws = quantize(c.w.to(dev))
-    ws = ws.reshape(-1).contiguous()
-    m, k = x.shape
-    n = wq.shape[0]
-    xq = torch.empty((m, k), dtype=torch.int8, device=dev)
-    xs = torch.empty((m,), dtype=torch.float32, device=dev)
-    out = torch.empty((m, n), dtype=torch.float16, device=dev)
-    s = torch.cuda.current_stream(dev)
-    P = _lib.ptr
+class Cfg0:
+    """BASELINE configuration 0 (M 4096, N = K = 3072, fp16 in / out, seed 0):
+    the per-token quantizer and the INT8 GEMM with the order-F epilogue and
+    bias, each launched through the C ABI on preallocated buffers."""
 
-    def quant():
-        _lib.check(lib.qg_quant_rows_i8(P(x), _lib.F16, k, 1, m, k, P(xq), k, P(xs), 0, s.cuda_stream), "q")
+    def __init__(self, torch, lib, _lib, quantize, synthetic, dev, iters=50):
+        self.t, self.lib, self.L, self.iters = torch, lib, _lib, iters
+        c = synthetic.cfg0()
+        self.x, self.bias = c.x.to(dev), c.bias.to(dev)
+        self.wq, ws = quantize(c.w.to(dev))
+        self.ws = ws.reshape(-1).contiguous()
+        self.m, self.k = self.x.shape
+        self.n = self.wq.shape[0]
+        self.xq = torch.empty((self.m, self.k), dtype=torch.int8, device=dev)
+        self.xs = torch.empty((self.m,), dtype=torch.float32, device=dev)
+        self.out = torch.empty((self.m, self.n), dtype=torch.float16, device=dev)
+        self.stream = torch.cuda.current_stream(dev)
+        for _ in range(5):
+            self.quant()
+            self.gemm()
+        torch.cuda.synchronize()
 
-    def gemm():
-        _lib.check(lib.qg_int8_gemm(P(xq), k, 1, P(wq), 1, k, m, n, k, P(xs), P(ws), n, P(bias), _lib.F16,
-                                    P(out), _lib.F16, 0, None, 0, s.cuda_stream), "g")
+    def quant(self):
+        P, L = self.L.ptr, self.L
+        L.check(self.lib.qg_quant_rows_i8(P(self.x), L.F16, self.k, 1, self.m, self.k, P(self.xq), self.k,
+                                          P(self.xs), L.ROUND_HALF_EVEN, self.stream.cuda_stream), "quant")
 
-    for _ in range(5):
-        quant(); gemm()
-    torch.cuda.synchronize()
-    res = {}
-    for label, fn in (("gemm", gemm), ("quant", quant)):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for _ in range(iters):
+    def gemm(self):
+        P, L, m, n, k = self.L.ptr, self.L, self.m, self.n, self.k
+        L.check(self.lib.qg_int8_gemm(P(self.xq), k, 1, P(self.wq), 1, k, m, n, k, P(self.xs), P(self.ws), n,
+                                      P(self.bias), L.F16, P(self.out), L.F16, 0, None, 0,
+                                      self.stream.cuda_stream), "gemm")
+
+    def _time(self, fn):
+        e0, e1 = self.t.cuda.Event(enable_timing=True), self.t.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(self.iters):
             fn()
-        e1.record(s)
+        e1.record(self.stream)
         e1.synchronize()
-        res[label] = e0.elapsed_time(e1) / iters
-    ops = 2.0 * m * n * k
-    gemm_tops = ops / (res["gemm"] * 1e-3) / 1e12
-    lin_tops = ops / ((res["gemm"] + res["quant"]) * 1e-3) / 1e12
-    quant_bytes = m * k * 2 + m * k + m * 4
-    return {"cfg0_gemm_us": round(res["gemm"] * 1e3, 2), "cfg0_gemm_tops": round(gemm_tops, 1),
-            "cfg0_gemm_frac_int8_peak": round(gemm_tops / PEAK_INT8_TOPS, 4),
-            "cfg0_quant_us": round(res["quant"] * 1e3, 2),
-            "cfg0_quant_gbs": round(quant_bytes / (res["quant"] * 1e-3) / 1e9, 1),
-            "cfg0_w8a8_linear_tops": round(lin_tops, 1)}
+        return e0.elapsed_time(e1) / self.iters
+
+    def time_gemm(self):
+        return self._time(self.gemm)
+
+    def time_quant(self):
+        return self._time(self.quant)
+
+    def ops(self):
+        return 2.0 * self.m * self.n * self.k
+
+    def quant_bytes(self):
+        return self.m * self.k * 2 + self.m * self.k + self.m * 4
+
+    def profile_run(self):
+        """One quant + GEMM pair after warm-up (for rocprofv3 runs)."""
+        ms = self.time_gemm()
+        return {"gemm_us": round(ms * 1e3, 2), "tops": round(self.ops() / (ms * 1e-3) / 1e12, 1)}
 
 
 def _graph_time(torch, fn, launches, replays=4):
@@ -176,51 +204,134 @@ def _graph_time(torch, fn, launches, replays=4):
     return e0.elapsed_time(e1) / (launches * replays)
 
 
-def run_w4a16(torch, lib, _lib, dev, copies=12):
-    """W4A16, K 4096, N 14336, group 128, uint4
-    storage with bf16 scales and uint4 zero points, bf16 activations / out.
-    Decode (M = 1, 16) rotates over ``copies`` weight copies (> 256 MB, more than
-    the MALL) so every launch streams its weights from HBM."""
+def _w4_weights(torch, dev, copies):
+    """BASELINE configuration 2 weights (K 4096, N 14336, g128, uint4 storage with
+    bf16 scales and packed uint4 zero points) and ``copies - 1`` clones."""
     from rdna2_ops import int4_weight_gemm_v07 as w4
     N, K, G = 14336, 4096, 128
     gen = torch.Generator().manual_seed(2)
     p0 = w4.pack_uint4((torch.randn(N, K, generator=gen) * 0.02).to(dev), group_size=G)
     ps = [p0] + [w4.PackedInt4(p0.data.clone(), p0.scales.clone(), p0.zeros.clone(), p0.sums, N, K, G, False,
                                signed=False, zeros_packed=True) for _ in range(copies - 1)]
-    wbytes = p0.data.numel() * 4 + p0.scales.numel() * 2 + p0.zeros.numel() * 4
-    P = _lib.ptr
+    return gen, ps
+
+
+class DecodeW4:
+    """The W4A16 decode shapes of BASELINE configuration 2 (M = 1 and 16, bf16
+    activations and output). Each sample is one replay of a HIP graph of 120
+    launches rotating over ``copies`` weight copies (366 MB, more than the
+    256 MB MALL), so every launch streams its weights from HBM; the time per
+    launch is the replay's event time / 120."""
+
+    N, K, G = 14336, 4096, 128
+
+    def __init__(self, torch, lib, _lib, dev, copies=12, launches=120):
+        self.t, self.lib, self.L, self.copies, self.launches = torch, lib, _lib, copies, launches
+        gen, self.ps = _w4_weights(torch, dev, copies)
+        p0 = self.ps[0]
+        self.wbytes = p0.data.numel() * 4 + p0.scales.numel() * 2 + p0.zeros.numel() * 4
+        self.graphs = {}
+        for m in (1, 16):
+            a = torch.randn(m, self.K, generator=gen).to(torch.bfloat16).to(dev)
+            y = torch.empty(m, self.N, dtype=torch.bfloat16, device=dev)
+            self.graphs[m] = self._capture(m, a, y)
+
+    def _call(self, m, a, y, p, stream):
+        P, L = self.L.ptr, self.L
+        L.check(self.lib.qg_w4a16_gemm(P(a), L.BF16, self.K, m, self.K, P(p.data), self.N, self.G, p.flags,
+                                       P(p.scales), L.BF16, P(p.zeros), None, 0, P(y), L.BF16, None, 0, stream),
+                "w4a16")
+
+    def _capture(self, m, a, y):
+        torch = self.t
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            for i in range(4):
+                self._call(m, a, y, self.ps[i % self.copies], s.cuda_stream)
+            s.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for i in range(self.launches):
+                    self._call(m, a, y, self.ps[i % self.copies], s.cuda_stream)
+            g.replay()
+            s.synchronize()
+        return g, s, a, y
+
+    def time(self, m):
+        g, s, _, _ = self.graphs[m]
+        torch = self.t
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / self.launches
+
+    def result(self, m, ms, samples):
+        nbytes = self.wbytes + m * self.K * 2 + m * self.N * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"us": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                "TFLOPs": round(2 * m * self.N * self.K / (ms * 1e-3) / 1e12, 1), "bytes": nbytes,
+                "us_by_round": [round(v * 1e3, 2) for v in samples]}
+
+    @staticmethod
+    def kernel_name(m):
+        return "k_w4_decode<RP=1,CT=2,G=128,uint4>" if m == 1 else "k_w4_decode<RP=16,CT=4,G=128,uint4>"
+
+
+def run_w4a16(torch, lib, _lib, dev, rows=(1, 16, 2048), copies=12):
+    """BASELINE configuration 2 at the given row counts, each the median of three
+    samples: decode rows (<= 16) through DecodeW4's rotated graphs, prefill
+    (2048) over one weight with graph replays of 10 launches; for 2048 also the
+    reference's default ``dequant`` method (this library's unpack to bf16, then
+    the library GEMM) with HIP events over eager calls."""
+    from rdna2_ops import int4_weight_gemm_v07 as w4
     out = {}
-    for m in (1, 16, 2048):
+    dec = [m for m in rows if m <= 16]
+    if dec:
+        d = DecodeW4(torch, lib, _lib, dev, copies=copies)
+        for m in dec:
+            samples = [d.time(m) for _ in range(3)]
+            out[m] = d.result(m, statistics.median(samples), samples)
+    if 2048 in rows:
+        N, K, G, m = 14336, 4096, 128, 2048
+        gen, ps = _w4_weights(torch, dev, 1)
+        p0 = ps[0]
+        wbytes = p0.data.numel() * 4 + p0.scales.numel() * 2 + p0.zeros.numel() * 4
         a = torch.randn(m, K, generator=gen).to(torch.bfloat16).to(dev)
         y = torch.empty(m, N, dtype=torch.bfloat16, device=dev)
+        P = _lib.ptr
 
-        def call(i, stream, a=a, y=y, m=m):
-            p = ps[i % copies] if m <= 16 else p0
-            _lib.check(lib.qg_w4a16_gemm(P(a), _lib.BF16, K, m, K, P(p.data), N, G, p.flags, P(p.scales), _lib.BF16,
-                                         P(p.zeros), None, 0, P(y), _lib.BF16, None, 0, stream), "w4a16")
-        ms = _graph_time(torch, call, 120 if m <= 16 else 10, replays=4 if m <= 16 else 2)
+        def call(i, stream):
+            _lib.check(lib.qg_w4a16_gemm(P(a), _lib.BF16, K, m, K, P(p0.data), N, G, p0.flags, P(p0.scales),
+                                         _lib.BF16, P(p0.zeros), None, 0, P(y), _lib.BF16, None, 0, stream),
+                       "w4a16")
+        ms = statistics.median([_graph_time(torch, call, 10, replays=2) for _ in range(3)])
         bytes_ = wbytes + m * K * 2 + m * N * 2
         out[m] = {"us": round(ms * 1e3, 2), "GBs": round(bytes_ / (ms * 1e-3) / 1e9, 1),
                   "frac_hbm_peak": round(bytes_ / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                  "TFLOPs": round(2 * m * N * K / (ms * 1e-3) / 1e12, 1), "bytes": bytes_}
-        if m == 2048:
-            # the reference's default method at the same shape: this library's
-            # unpack to bf16, then the library (hipBLASLt) GEMM, HIP events over
-            # eager calls (the reference API is eager-only)
-            def dequant(a=a):
-                return w4.int4_linear_a16(a, p0, method="dequant")
-            for _ in range(3):
-                dequant()
-            torch.cuda.synchronize()
+                  "TFLOPs": round(2 * m * N * K / (ms * 1e-3) / 1e12, 1),
+                  "frac_bf16_peak": round(2 * m * N * K / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                  "bytes": bytes_}
+
+        def dequant():
+            return w4.int4_linear_a16(a, p0, method="dequant")
+        for _ in range(3):
+            dequant()
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(3):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(10):
                 dequant()
             e1.record()
             torch.cuda.synchronize()
-            dms = e0.elapsed_time(e1) / 10
-            out["2048_dequant_method"] = {"us": round(dms * 1e3, 2),
-                                          "TFLOPs": round(2 * m * N * K / (dms * 1e-3) / 1e12, 1)}
+            samples.append(e0.elapsed_time(e1) / 10)
+        dms = statistics.median(samples)
+        out["2048_dequant_method"] = {"us": round(dms * 1e3, 2),
+                                      "TFLOPs": round(2 * m * N * K / (dms * 1e-3) / 1e12, 1)}
     return out
 
 
@@ -245,7 +356,7 @@ def run_fp8(torch, lib, _lib, dev):
         def call(i, stream, a=a, y=y, codes=codes, sc=sc, n=n, ws=ws, wsb=wsb):
             _lib.check(lib.qg_fp8w_gemm(P(a), _lib.BF16, k, 1, m, k, P(codes), _lib.E4M3, k, 1, n, P(sc), None, 0,
                                         P(y), _lib.BF16, P(ws) if wsb else None, wsb, stream), "fp8w")
-        ms = _graph_time(torch, call, 10, replays=2)
+        ms = statistics.median([_graph_time(torch, call, 10, replays=2) for _ in range(3)])
         tf = 2 * m * n * k / (ms * 1e-3) / 1e12
         res[n] = {"us": round(ms * 1e3, 1), "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
         # the reference's decode method: this library's fp8 -> bf16 decode,
@@ -257,13 +368,16 @@ def run_fp8(torch, lib, _lib, dev):
         for _ in range(3):
             decode()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(10):
-            decode()
-        e1.record()
-        torch.cuda.synchronize()
-        dms = e0.elapsed_time(e1) / 10
+        dsamples = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                decode()
+            e1.record()
+            torch.cuda.synchronize()
+            dsamples.append(e0.elapsed_time(e1) / 10)
+        dms = statistics.median(dsamples)
         res[f"{n}_decode_method_unscaled"] = {"us": round(dms * 1e3, 1), "TFLOPs": round(2 * m * n * k / (dms * 1e-3) / 1e12, 1)}
     return res
 
@@ -283,13 +397,16 @@ def run_moe(torch, dev, iters=20):
         moe_int8.moe_int8_forward(x, lg, prep, top_k=c.top_k)
     torch.cuda.synchronize()
     s = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s)
-    for _ in range(iters):
-        moe_int8.moe_int8_forward(x, lg, prep, top_k=c.top_k)
-    e1.record(s)
-    e1.synchronize()
-    ms = e0.elapsed_time(e1) / iters
+    samples = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(iters):
+            moe_int8.moe_int8_forward(x, lg, prep, top_k=c.top_k)
+        e1.record(s)
+        e1.synchronize()
+        samples.append(e0.elapsed_time(e1) / iters)
+    ms = statistics.median(samples)
     t, h = c.x.shape
     e, f = c.w_gate.shape[0], c.w_gate.shape[1]
     ops = 2.0 * t * c.top_k * (h * 2 * f + f * h)
@@ -318,28 +435,104 @@ def run_w4a8(torch, dev, iters=20):
             w4.int4_linear_a8(a, p, sa)
         torch.cuda.synchronize()
         s = torch.cuda.current_stream(dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for _ in range(iters):
-            w4.int4_linear_a8(a, p, sa)
-        e1.record(s)
-        e1.synchronize()
-        us = e0.elapsed_time(e1) / iters * 1e3
+        samples = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(iters):
+                w4.int4_linear_a8(a, p, sa)
+            e1.record(s)
+            e1.synchronize()
+            samples.append(e0.elapsed_time(e1) / iters)
+        us = statistics.median(samples) * 1e3
         tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
         res[label] = {"us": round(us, 1), "TOPS": round(tops, 1), "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4),
                       "shape": [m, n, k], "group": g}
     return res
 
 
-def traffic_bytes(name="int8_gemm_cfg1_chain_traffic.json"):
-    """HBM bytes per launch of a kernel, measured with rocprofv3 --pmc
-    FETCH_SIZE / WRITE_SIZE (scaled by a plain-copy calibration) and recorded in
-    profiles/<name>; None if absent."""
+def traffic_record(name):
+    """HBM bytes per launch of a kernel, from rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE runs (each scaled by the same counter's reading for a plain copy
+    of known size) recorded in profiles/<name>, with where they came from;
+    (None, None) if absent. The counters cannot be read inside this process,
+    so the figure is the one of the last profiling run of that kernel."""
     path = ROOT / "profiles" / name
     try:
-        return json.loads(path.read_text())["hbm_bytes_per_launch"]
+        rec = json.loads(path.read_text())
+        return rec["hbm_bytes_per_launch"], {"file": "profiles/" + name, "kernel": rec.get("kernel"),
+                                             "measured": rec.get("measured")}
     except (OSError, KeyError, ValueError):
-        return None
+        return None, None
+
+
+class ClockSampler:
+    """Samples the GPU's current GFX (shader) clock with amdsmi from a host
+    thread while the timed rounds run; the samples show the clock the kernels
+    ran at (the MFMA peak assumes 2.4 GHz). Reports nothing if amdsmi cannot
+    read the clock on this box."""
+
+    def __init__(self, period_s=0.002):
+        self.period = period_s
+        self.samples = []
+        self.error = None
+        self._stop = None
+        self._thread = None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self._smi = amdsmi
+            self._handle = amdsmi.amdsmi_get_processor_handles()[0]
+            amdsmi.amdsmi_get_clock_info(self._handle, amdsmi.AmdSmiClkType.GFX)
+        except Exception as e:  # no amdsmi, no permission, no device
+            self._smi = None
+            self.error = f"{type(e).__name__}: {e}"
+
+    def __enter__(self):
+        import threading
+        if self._smi is None:
+            return self
+        self._stop = threading.Event()
+
+        def run():
+            while not self._stop.is_set():
+                try:
+                    info = self._smi.amdsmi_get_clock_info(self._handle, self._smi.AmdSmiClkType.GFX)
+                    self.samples.append(float(info.get("clk", info.get("cur_clk", 0))))
+                except Exception as e:
+                    self.error = f"{type(e).__name__}: {e}"
+                    return
+                self._stop.wait(self.period)
+        self._thread = threading.Thread(target=run, daemon=True)
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join()
+        return False
+
+    def summary(self):
+        if not self.samples:
+            return {"source": "amdsmi GFX clock", "available": False, "error": self.error}
+        s = sorted(self.samples)
+        return {"source": "amdsmi GFX clock, sampled every 2 ms by a host thread during the timed rounds",
+                "available": True, "median_mhz": s[len(s) // 2], "min_mhz": s[0], "max_mhz": s[-1],
+                "samples": len(s)}
+
+
+def alternating_rounds(items, rounds):
+    """The reference's timing protocol (rdna2-ops/bench_int8_gemm.py:259-268):
+    every round times every item once, in list order on even rounds and in
+    reverse order on odd ones; each item's result is the median over rounds.
+    ``items`` maps a name to a callable returning one sample (ms)."""
+    samples = {name: [] for name in items}
+    names = list(items)
+    for r in range(rounds):
+        for name in (names if r % 2 == 0 else names[::-1]):
+            samples[name].append(items[name]())
+    return {name: (statistics.median(v), v) for name, v in samples.items()}
 
 
 def main():
@@ -348,6 +541,9 @@ def main():
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(run with --gpus 1; sharding is described in DESIGN.md)", file=sys.stderr, flush=True)
+        sys.exit(2)
+    if args.rounds < 1:
+        print("--rounds must be at least 1", file=sys.stderr, flush=True)
         sys.exit(2)
     import torch
     from rdna2_ops import _lib, synthetic
@@ -367,7 +563,9 @@ def main():
     lib = _lib.library()
     if args.only:
         runs = {"w4a16": lambda: run_w4a16(torch, lib, _lib, dev), "fp8": lambda: run_fp8(torch, lib, _lib, dev),
-                "moe": lambda: run_moe(torch, dev), "w4a8": lambda: run_w4a8(torch, dev)}
+                "moe": lambda: run_moe(torch, dev), "w4a8": lambda: run_w4a8(torch, dev),
+                "cfg0": lambda: Cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev).profile_run(),
+                "decode": lambda: run_w4a16(torch, lib, _lib, dev, rows=(1,))}
         res = runs[args.only]()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return
@@ -377,30 +575,46 @@ def main():
     torch.cuda.synchronize()
 
     events = []
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(chain.stream)
-    for _ in range(args.steps):
-        chain.step(events)
-    stop.record(chain.stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / args.steps
+
+    def chain_round():
+        """Exactly --steps chain steps between two synchronisations; ms per step."""
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(chain.stream)
+        for _ in range(args.steps):
+            chain.step(events)
+        stop.record(chain.stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / args.steps
+
+    items = {"chain": chain_round}
+    cfg0 = decode = None
+    if not args.no_secondary:
+        cfg0 = Cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev)
+        decode = DecodeW4(torch, lib, _lib, dev)
+        items.update(cfg0_gemm=cfg0.time_gemm, cfg0_quant=cfg0.time_quant,
+                     w4a16_m1=lambda: decode.time(1), w4a16_m16=lambda: decode.time(16))
+    with ClockSampler() as clock:
+        timed = alternating_rounds(items, args.rounds)
+    ms, chain_samples = timed["chain"]
     ops = chain.ops()
     value = ops / (ms * 1e-3) / 1e12
 
-    gemm_ms = sum(e0.elapsed_time(e1) for _, e0, e1 in events)
-    gemm_ops = ops * args.steps
+    # the dominant kernel: each GEMM launch of the chain bracketed by events on
+    # its stream, every step of every round
     per_layer = {}
     for i, e0, e1 in events:
         per_layer.setdefault(i, []).append(e0.elapsed_time(e1))
-    achieved = gemm_ops / (gemm_ms * 1e-3) / 1e12
+    gemm_ms_per_step = sum(statistics.median(v) for v in per_layer.values())
+    achieved = ops / (gemm_ms_per_step * 1e-3) / 1e12
     layer_info = {}
     for i, name in enumerate(("qkv", "up_gelu", "down")):
         L = chain.layers[i]
-        t = sum(per_layer[i]) / len(per_layer[i])
+        t = statistics.median(per_layer[i])
         layer_info[name] = {"us": round(t * 1e3, 2),
                             "tops": round(2 * chain.m * L["n"] * L["k"] / (t * 1e-3) / 1e12, 1)}
+    traffic, traffic_src = traffic_record("int8_gemm_cfg1_chain_traffic.json")
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "TOPS", "n_gpus": 1,
@@ -411,25 +625,48 @@ def main():
                                "QKV N=9216; MLP up N=12288 + GELU-tanh; MLP down K=12288->N=3072; "
                                "per-token int8 quant prologue on each GEMM; fp16 in/out",
                    "tokens": chain.m, "hidden": 3072, "ops_per_step": ops},
+        "protocol": {"rounds": args.rounds, "order": "alternating (forward on even rounds, reverse on odd)",
+                     "statistic": "median over rounds", "steps_per_round": args.steps,
+                     "chain_ms_per_step_by_round": [round(v, 5) for v in chain_samples]},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS,
-                     "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic_bytes(),
+                     "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": "k_i8_gemm_pp<256x192 tile, 8 waves> (int8 MFMA GEMM, ping-pong main loop, fused epilogue, persistent grid)",
                      "per_launch": layer_info},
+        "clock": clock.summary(),
     }
     if not args.no_secondary:
-        sec = run_cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev)
-        w4 = run_w4a16(torch, lib, _lib, dev)
+        g_ms, g_s = timed["cfg0_gemm"]
+        q_ms, q_s = timed["cfg0_quant"]
+        cfg0_ops = cfg0.ops()
+        g_tops = cfg0_ops / (g_ms * 1e-3) / 1e12
+        c0_traffic, c0_src = traffic_record("int8_gemm_cfg0_traffic.json")
+        # the >= 60 % bar of the metric is quoted on configuration 0
+        line["roofline_cfg0"] = {
+            "bound": "mfma", "achieved": round(g_tops, 1), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+            "frac": round(g_tops / PEAK_INT8_TOPS, 4), "traffic": c0_traffic, "traffic_source": c0_src,
+            "kernel": "k_i8_gemm_pp<256x192 tile, 8 waves> (M=4096, N=K=3072, fp16 out, order F + bias)",
+            "us_per_launch": round(g_ms * 1e3, 2), "us_by_round": [round(v * 1e3, 2) for v in g_s]}
+        sec = {"cfg0_gemm_us": round(g_ms * 1e3, 2), "cfg0_gemm_tops": round(g_tops, 1),
+               "cfg0_gemm_frac_int8_peak": round(g_tops / PEAK_INT8_TOPS, 4),
+               "cfg0_quant_us": round(q_ms * 1e3, 2),
+               "cfg0_quant_gbs": round(cfg0.quant_bytes() / (q_ms * 1e-3) / 1e9, 1),
+               "cfg0_w8a8_linear_tops": round(cfg0_ops / ((g_ms + q_ms) * 1e-3) / 1e12, 1)}
+        w4 = {m: decode.result(m, *timed[f"w4a16_m{m}"]) for m in (1, 16)}
         dec = w4[1]
+        d_traffic, d_src = traffic_record("w4a16_decode_cfg2_traffic.json")
         # second half of the headline metric: W4A16 decode (M = 1) HBM GB/s
         line["roofline_w4a16_decode"] = {
             "bound": "hbm", "achieved": dec["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": dec["frac_hbm_peak"], "traffic": traffic_bytes("w4a16_decode_cfg2_traffic.json"),
-            "kernel": "k_w4_decode<1,2,128> (M=1, K 4096, N 14336, g128 uint4, 12 rotated weight copies)",
-            "us_per_launch": dec["us"], "algorithmic_bytes": dec["bytes"]}
+            "frac": dec["frac_hbm_peak"], "traffic": d_traffic, "traffic_source": d_src,
+            "kernel": decode.kernel_name(1) + " (M=1, K 4096, N 14336, g128 uint4, "
+                      f"{decode.copies} rotated weight copies)",
+            "us_per_launch": dec["us"], "us_by_round": dec["us_by_round"], "algorithmic_bytes": dec["bytes"]}
         sec["w4a16_m1"] = w4[1]
         sec["w4a16_m16"] = w4[16]
-        sec["w4a16_prefill_m2048"] = w4[2048]
-        sec["w4a16_prefill_m2048_dequant_method"] = w4["2048_dequant_method"]
+        pre = run_w4a16(torch, lib, _lib, dev, rows=(2048,))
+        sec["w4a16_prefill_m2048"] = pre[2048]
+        sec["w4a16_prefill_m2048_dequant_method"] = pre["2048_dequant_method"]
         sec["fp8_cfg3"] = run_fp8(torch, lib, _lib, dev)
         sec["moe_cfg4"] = run_moe(torch, dev)
         sec["w4a8"] = run_w4a8(torch, dev)

@@ -447,8 +447,12 @@ Fp8Plan plan_fp8(const void* a, int64_t a_sm, int64_t a_sk, const void* w, int64
                  int64_t m, int64_t n, int64_t k) {
   Fp8Plan pl;
   pl.kp = round_up(k, kStageK);
-  pl.pack_a = !(a_sk == 1 && a_sm % 8 == 0 && aligned16(a) && k % kStageK == 0);
-  pl.pack_w = !(w_sk == 1 && w_sn % 16 == 0 && aligned16(w) && k % kStageK == 0);
+  // In place only when every row's byte offset fits the kernels' 32-bit
+  // offsets: the span of the last row ends below 2 GiB.
+  pl.pack_a = !(a_sk == 1 && a_sm % 8 == 0 && aligned16(a) && k % kStageK == 0 &&
+                2 * ((m - 1) * a_sm + k) < kMaxOperandBytes);
+  pl.pack_w = !(w_sk == 1 && w_sn % 16 == 0 && aligned16(w) && k % kStageK == 0 &&
+                (n - 1) * w_sn + k < kMaxOperandBytes);
   pl.a_bytes = pl.pack_a ? static_cast<size_t>(round_up(2 * m * pl.kp, 256)) : 0;
   pl.w_bytes = pl.pack_w ? static_cast<size_t>(round_up(n * pl.kp, 256)) : 0;
   // >= 192 tiles of 256 x 192 (the INT8 kernel's large-grid rule) and the

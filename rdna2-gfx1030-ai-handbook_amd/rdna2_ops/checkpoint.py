@@ -12,12 +12,15 @@ the MOSS node passes), so an INT8 checkpoint needs no converted copy at all;
 converted layouts (packed W4, fp8 views) come from ``ResidentWeights``, whose
 entries carry an explicit validity contract:
 
-* an entry is the prepared copy of one source tensor together with the
-  source's signature — device, dtype, shape, strides, data pointer and
-  in-place version counter (``Tensor._version``);
-* ``get`` returns the entry only while the signature is unchanged and
-  prepares it again otherwise (an in-place update such as a LoRA merge bumps
-  the version; a reload or offload round trip changes the pointer);
+* an entry is the prepared copy of one source tensor together with a weak
+  reference to the source's storage object and the source's signature —
+  device, dtype, shape, strides, data pointer and in-place version counter
+  (``Tensor._version``);
+* ``get`` returns the entry only while the referenced storage is the
+  source's and the signature is unchanged, and prepares it again otherwise
+  (an in-place update such as a LoRA merge bumps the version; a reload or
+  offload round trip is a new storage, even when the allocator places it at
+  the old address with version 0);
 * ``invalidate(key)`` / ``clear()`` drop entries explicitly — a caller that
   replaces a weight's contents by a route that keeps pointer and version (a
   raw device copy from outside PyTorch) must call it.
@@ -30,6 +33,7 @@ import hashlib
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Callable, Dict, Optional
+import weakref
 
 import torch
 
@@ -140,8 +144,16 @@ def _signature(t: torch.Tensor):
 class ResidentWeights:
     """Prepared copies of source weights with the validity contract in the
     module docstring. ``prepare(source) -> prepared`` makes the copy (e.g. a
-    W4 packing); ``get(key, source)`` returns the cached copy while the
-    source's signature is unchanged and prepares it again otherwise."""
+    W4 packing); ``get(key, source)`` returns the cached copy only while the
+    source is the same storage, unchanged, and prepares it again otherwise.
+
+    "The same storage" is a weak reference to the source's storage object,
+    not its address: a weight that is freed (offloaded) and reloaded is a new
+    storage with in-place version 0, and the caching allocator often places it
+    at the old address, so address, shape, strides and version alone would
+    return the stale copy (the reference rejects address-keyed caches for this
+    reason, production/README.md:96-101). A dead or different referent is a
+    miss. The weak reference keeps nothing alive."""
 
     def __init__(self, prepare: Callable[[torch.Tensor], object]):
         self._prepare = prepare
@@ -149,15 +161,15 @@ class ResidentWeights:
         self.prepared = 0  # number of prepare calls (for tests and statistics)
 
     def get(self, key: str, source: torch.Tensor):
-        sig = _signature(source)
+        storage = source.untyped_storage()
         entry = self._entries.get(key)
-        if entry is not None and entry[0] == sig:
-            return entry[1]
+        if entry is not None and entry[1]() is storage and entry[0] == _signature(source):
+            return entry[2]
         value = self._prepare(source)
         self.prepared += 1
         # the signature after preparing: a prepare that reads the source does
         # not change it; one that modified it in place is caught next time
-        self._entries[key] = (_signature(source), value)
+        self._entries[key] = (_signature(source), weakref.ref(storage), value)
         return value
 
     def invalidate(self, key: Optional[str] = None) -> None:

@@ -14,7 +14,14 @@ Triton launch knobs (tile, num_warps, num_stages, group_m, wrapped,
 partial_dot) are accepted and validated exactly as the reference does
 (int8_gemm.py:144-147, :155-156) so callers keep working; on MI355X they are
 hints only — the library picks its own MFMA tile — and results never depend
-on them (integer accumulation is exact; the epilogue is per element).
+on them: integer accumulation is exact and the epilogue is per element.
+``wrapped`` asks for the reference's variant that loads the unused rows and
+columns of edge tiles from valid indices and masks only the stores
+(int8_gemm.py:70-123); every kernel of this library already loads edge rows
+from clamped, valid indices, so both settings run the same kernel.
+``partial_dot`` (the wrapped variant's acc += dot form, :103-106) adds exact
+int32 partial products, the same sums. The returned kernel metadata records
+both requests.
 
 New keyword arguments (defaults keep the reference's behaviour):
 ``out_dtype`` (fp32 default; fp16/bf16 round the fp32 epilogue once, RNE),
@@ -27,7 +34,7 @@ import sys
 
 import torch
 
-from . import _lib
+from . import _kitchen, _lib
 
 _MAX_K = 131071
 
@@ -132,7 +139,8 @@ def _launch(a, b, a_scale, b_scale, bias, *, tile, num_warps, num_stages, group_
     tile_used = (256, 192, 128) if big else (128, 128, 128)
     meta = _lib.kernel_metadata("int8_mfma_32x32x32_pingpong" if big else "int8_mfma_32x32x32", tile_used,
                                 "k_i8_gemm_ppINS0_5I8GeoILi256ELi192E" if big else "k_i8_gemmINS0_5I8GeoILi128ELi128E")
-    meta.update(packed_operands=ws_bytes > 0, requested_tile=list(tile), epilogue_flags=flags)
+    meta.update(packed_operands=ws_bytes > 0, requested_tile=list(tile), epilogue_flags=flags,
+                requested_wrapped=bool(wrapped), requested_partial_dot=bool(partial_dot))
     return out, meta
 
 
@@ -224,119 +232,119 @@ def w8a8_linear(x, weight, weight_scale, bias=None, *, out_dtype=None, activatio
     return out.reshape(*x.shape[:-1], n)
 
 
+def _research_knobs(tile, num_warps, num_stages, group_m, wrapped, partial_dot):
+    return dict(tile=tile, num_warps=num_warps, num_stages=num_stages, group_m=group_m, wrapped=wrapped,
+                partial_dot=partial_dot)
+
+
 @contextmanager
 def moss_int8_gemm_candidate(*, tile=(32, 64, 64), num_warps=4,
                              num_stages=1, group_m=4, wrapped=False, partial_dot=False):
-    """Scoped MOSS eager export replacement in an exclusively owned process.
+    """Scoped MOSS research export: Kitchen's eager backend exports a linear whose
+    INT8 product and fp32 epilogue are one ``int8_gemm_dequant`` launch in the
+    reference order (rounding="separate": f32(acc) * (sa * sw), then + bias).
 
-    Mirrors rdna2-ops/rdna2_ops/int8_gemm.py:217-271: preserves Kitchen's input
-    activation, ConvRot, row quantizer and residual helpers; FP32 input/output
-    only; all other calls use the saved exported callable. No registry, code
-    object, source file or model weight is changed.
+    Interface of rdna2-ops/rdna2_ops/int8_gemm.py:217-271. fp32 activations
+    with fp32 output are served; every other call goes to the saved Kitchen
+    export and counts as a fallback. Kitchen's input activation, ConvRot,
+    quantizer and residual run unchanged around the product. Yields the
+    per-context counters {"hits", "fallbacks", "shapes"}. On exit the saved
+    export is restored, unless someone else replaced the candidate meanwhile
+    (RuntimeError). For an exclusively owned process: no registry entry, code
+    object, file or weight is changed.
     """
     from comfy_kitchen.backends import eager as backend
-    from comfy_kitchen.backends.eager import quantization as q
-    original = backend.int8_linear
-    stats = {"hits": 0, "fallbacks": 0, "shapes": {}}
+    from comfy_kitchen.backends.eager import quantization as kitchen
+    saved = backend.int8_linear
+    stats = _kitchen.CallStats()
+    knobs = _research_knobs(tile, num_warps, num_stages, group_m, wrapped, partial_dot)
 
-    def candidate(x, weight, weight_scale, bias=None, out_dtype=torch.bfloat16,
-                  convrot=False, convrot_groupsize=256, input_act=None,
-                  input_act_weight=None, input_act_eps=0.0,
+    def product(x_8, x_scale, weight, scale, bias):
+        b32 = None if bias is None else bias.to(device=x_8.device, dtype=torch.float32).reshape(-1)
+        y = int8_gemm_dequant(x_8, weight.T, x_scale, scale, b32, rounding="separate", **knobs)
+        stats.hit(x_8.shape[0], weight.shape[0], x_8.shape[1])
+        return y
+
+    def candidate(x, weight, weight_scale, bias=None, out_dtype=torch.bfloat16, convrot=False,
+                  convrot_groupsize=256, input_act=None, input_act_weight=None, input_act_eps=0.0,
                   residual=None, residual_scale=None):
+        options = dict(bias=bias, convrot=convrot, convrot_groupsize=convrot_groupsize, input_act=input_act,
+                       input_act_weight=input_act_weight, input_act_eps=input_act_eps, residual=residual,
+                       residual_scale=residual_scale)
         if x.dtype != torch.float32 or out_dtype != torch.float32:
-            stats["fallbacks"] += 1
-            return original(x, weight, weight_scale, bias=bias, out_dtype=out_dtype,
-                            convrot=convrot, convrot_groupsize=convrot_groupsize,
-                            input_act=input_act, input_act_weight=input_act_weight,
-                            input_act_eps=input_act_eps, residual=residual,
-                            residual_scale=residual_scale)
-        x = q._apply_input_act(x, input_act, input_act_weight, input_act_eps)
-        if x.shape[-1] != weight.shape[-1]:
-            raise ValueError("Input and weight inner dimensions differ")
-        weight = weight.to(device=x.device).contiguous()
-        ws = weight_scale.to(device=x.device, dtype=torch.float32).reshape(-1)
-        if ws.numel() not in (1, weight.shape[0]):
-            raise ValueError("Weight scale must be scalar or per output channel")
-        if convrot:
-            if x.shape[-1] % convrot_groupsize:
-                raise ValueError("ConvRot group size does not divide K")
-            h = q._build_hadamard(convrot_groupsize, device=x.device, dtype=x.dtype)
-            x = q._rotate_activation(x, h, convrot_groupsize)
-        shape = x.shape
-        a, sa = q.quantize_int8_rowwise(x.reshape(-1, shape[-1]))
-        bias32 = None if bias is None else bias.to(device=x.device, dtype=torch.float32).reshape(-1)
-        y = int8_gemm_dequant(a, weight.T, sa, ws, bias32, tile=tile,
-                              num_warps=num_warps, num_stages=num_stages,
-                              group_m=group_m, rounding="separate", wrapped=wrapped,
-                              partial_dot=partial_dot)
-        stats["hits"] += 1
-        key = str((a.shape[0], weight.shape[0], a.shape[1]))
-        stats["shapes"][key] = stats["shapes"].get(key, 0) + 1
-        return q._apply_residual(y.reshape(*shape[:-1], weight.shape[0]), residual, residual_scale)
+            stats.fallback()
+            return saved(x, weight, weight_scale, out_dtype=out_dtype, **options)
+        return _kitchen.fp32_linear(kitchen, x, weight, weight_scale, product=product, **options)
 
-    backend.int8_linear = candidate
-    try:
-        yield stats
-    finally:
-        if backend.int8_linear is not candidate:
-            raise RuntimeError("MOSS eager export changed during the research context")
-        backend.int8_linear = original
+    with _kitchen.swapped(backend, {"int8_linear": candidate},
+                          "MOSS eager export changed during the research context"):
+        yield stats.data
+
+
+# Source file of the patientx Qwen INT8 bridge (an external ComfyUI node)
+# whose two GEMM wrappers the patientx candidate replaces.
+_PATIENTX_BRIDGE = "RDNA2-Qwen21-INT8/rocm_int8_kitchen_patch.py"
+_PATIENTX_WRAPPERS = ("triton_int8_linear", "triton_int8_linear_per_row")
+
+
+def _loaded_patientx_bridge():
+    hits = [mod for mod in tuple(sys.modules.values())
+            if mod is not None and str(getattr(mod, "__file__", "")).endswith(_PATIENTX_BRIDGE)]
+    if len(hits) != 1:
+        raise RuntimeError("Expected one already-loaded Qwen patientx bridge")
+    return hits[0]
+
+
+def _patientx_weight_scale(weight_scale, weight, device, per_row):
+    """The fp32 column-scale vector patientx hands its GEMM (int8_gemm.py:304-309):
+    the per-row wrapper's [N] view, a tensor scale moved to the device, or a
+    Python number as a one-element tensor."""
+    if per_row:
+        return weight_scale.reshape(weight.shape[0]).contiguous()
+    if isinstance(weight_scale, torch.Tensor):
+        return weight_scale.to(device, non_blocking=True).reshape(-1)
+    return torch.tensor([weight_scale], device=device, dtype=torch.float32)
 
 
 @contextmanager
 def qwen_int8_gemm_candidate(patch_module=None, *, tile=(32, 64, 64),
                              num_warps=4, num_stages=1, group_m=4, wrapped=False, partial_dot=False):
-    """Scoped replacement of the patientx bridge's two GEMM wrappers.
+    """Scoped replacement of the patientx bridge's two GEMM wrappers
+    (``triton_int8_linear`` and ``triton_int8_linear_per_row``) by
+    ``int8_gemm_dequant`` with the FMA epilogue (rounding="fused":
+    fma(f32(acc), sa * sw, bias), the patientx Triton behaviour).
 
-    Mirrors rdna2-ops/rdna2_ops/int8_gemm.py:274-330. The original patientx row
-    quantizer stays in use; the epilogue uses FMA rounding like patientx.
+    Interface of rdna2-ops/rdna2_ops/int8_gemm.py:274-330. The bridge module
+    is found among the loaded modules by its source path unless given; its own
+    row quantizer (``triton_quantize_rowwise`` in the wrapper's globals) stays
+    in use. fp32 input with compute_dtype fp32 is served, every other call goes
+    to the saved wrapper (a fallback). Yields {"hits", "fallbacks", "shapes"};
+    on exit both wrappers are restored, unless either was replaced meanwhile
+    (RuntimeError).
     """
-    if patch_module is None:
-        found = [mod for mod in tuple(sys.modules.values()) if mod is not None
-                 and str(getattr(mod, "__file__", "")).endswith(
-                     "RDNA2-Qwen21-INT8/rocm_int8_kitchen_patch.py")]
-        if len(found) != 1:
-            raise RuntimeError("Expected one already-loaded Qwen patientx bridge")
-        patch_module = found[0]
-    originals = {name: getattr(patch_module, name) for name in
-                 ("triton_int8_linear", "triton_int8_linear_per_row")}
-    stats = {"hits": 0, "fallbacks": 0, "shapes": {}}
-    replacements = {}
+    bridge = _loaded_patientx_bridge() if patch_module is None else patch_module
+    stats = _kitchen.CallStats()
+    knobs = _research_knobs(tile, num_warps, num_stages, group_m, wrapped, partial_dot)
 
-    def make_wrapper(original, per_row):
-        quantize = original.__globals__["triton_quantize_rowwise"]
+    def replacement_for(name):
+        saved = getattr(bridge, name)
+        per_row = name.endswith("_per_row")
+        quantize = saved.__globals__["triton_quantize_rowwise"]
 
         def candidate(x, weight, weight_scale, bias=None, compute_dtype=torch.float16):
             if x.dtype != torch.float32 or compute_dtype != torch.float32:
-                stats["fallbacks"] += 1
-                return original(x, weight, weight_scale, bias=bias, compute_dtype=compute_dtype)
-            shape = x.shape
-            x2d = x.reshape(-1, shape[-1])
-            a, sa = quantize(x2d.float() if per_row else x2d)
-            if per_row:
-                ws = weight_scale.reshape(weight.shape[0]).contiguous()
-            elif isinstance(weight_scale, torch.Tensor):
-                ws = weight_scale.to(x.device, non_blocking=True).reshape(-1)
-            else:
-                ws = torch.tensor([weight_scale], device=x.device, dtype=torch.float32)
-            y = int8_gemm_dequant(a, weight.T, sa, ws, bias, tile=tile,
-                                  num_warps=num_warps, num_stages=num_stages,
-                                  group_m=group_m, rounding="fused", wrapped=wrapped,
-                                  partial_dot=partial_dot)
-            stats["hits"] += 1
-            key = str((a.shape[0], weight.shape[0], a.shape[1]))
-            stats["shapes"][key] = stats["shapes"].get(key, 0) + 1
-            return y.reshape(*shape[:-1], weight.shape[0])
+                stats.fallback()
+                return saved(x, weight, weight_scale, bias=bias, compute_dtype=compute_dtype)
+            lead, k = x.shape[:-1], x.shape[-1]
+            rows = x.reshape(-1, k)
+            a, sa = quantize(rows.float() if per_row else rows)
+            ws = _patientx_weight_scale(weight_scale, weight, x.device, per_row)
+            y = int8_gemm_dequant(a, weight.T, sa, ws, bias, rounding="fused", **knobs)
+            stats.hit(a.shape[0], weight.shape[0], a.shape[1])
+            return y.reshape(*lead, weight.shape[0])
+
         return candidate
 
-    for name, original in originals.items():
-        replacements[name] = make_wrapper(original, name.endswith("per_row"))
-        setattr(patch_module, name, replacements[name])
-    try:
-        yield stats
-    finally:
-        for name in originals:
-            if getattr(patch_module, name) is not replacements[name]:
-                raise RuntimeError("Qwen patientx callable changed during the research context")
-        for name, original in originals.items():
-            setattr(patch_module, name, original)
+    with _kitchen.swapped(bridge, {name: replacement_for(name) for name in _PATIENTX_WRAPPERS},
+                          "Qwen patientx callable changed during the research context"):
+        yield stats.data

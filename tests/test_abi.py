@@ -107,3 +107,21 @@ def test_w4a8_gemm_rejects_invalid_arguments(lib):
     assert call(integer=2) == INVALID
     assert call(prepared=p, prepared_sn=100) == INVALID    # prepared rows on 16-byte boundaries
     assert call(m=0) == 0                                  # empty output: nothing to launch
+
+
+def test_fp8w_gemm_packs_rows_past_32bit_offsets(lib):
+    """Rows whose byte offsets do not fit the kernels' 32-bit offsets are packed
+    into workspace, never read in place (the offset would wrap to another row);
+    without that workspace the call is refused before any HIP call."""
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    m, n, k = 4, 300, 128
+    need_ok = lib.qg_fp8w_gemm_workspace_bytes(p, k, 1, p, k, 1, m, n, k)
+    assert need_ok == 0                                    # canonical rows: read in place
+    w_sn = 1 << 23                                         # (n - 1) * w_sn + k > 2^31
+    need = lib.qg_fp8w_gemm_workspace_bytes(p, k, 1, p, w_sn, 1, m, n, k)
+    assert need >= n * k                                   # W packed
+    a_sm = 1 << 22                                         # m = 300: 2 * ((m - 1) * a_sm + k) > 2^31
+    need_a = lib.qg_fp8w_gemm_workspace_bytes(p, a_sm, 1, p, k, 1, 300, n, k)
+    assert need_a >= 2 * 300 * k                           # A packed
+    base = [p, _lib.BF16, k, 1, m, k, p, _lib.E4M3, w_sn, 1, n, None, None, 0, p, _lib.BF16, None, 0, None]
+    assert lib.qg_fp8w_gemm(*base) == INVALID              # packing needs workspace

@@ -47,3 +47,33 @@ def test_w4_converter_resident_copy(cuda):
     wf.mul_(2)  # an in-place update (a LoRA merge, say): re-packed on next use
     p2 = conv.get("layer", wf)
     assert conv.prepared == 2 and torch.equal(p2.data, w4.pack_uint4(wf, group_size=128).data)
+
+
+def test_resident_copy_misses_a_reloaded_weight_at_the_same_address(cuda):
+    """A weight freed and re-allocated with other values (an offload round trip,
+    a LoRA merged on the CPU) may land at the same address with version 0; the
+    storage reference makes that a miss instead of a stale packed copy."""
+    from rdna2_ops import checkpoint as ck
+    from rdna2_ops import int4_weight_gemm_v07 as w4
+    case("checkpoint w4 converter reload at the same address")
+    conv = ck.w4_converter(group_size=128, uint4=True)
+    g = torch.Generator().manual_seed(6)
+    host_a = torch.randn(256, 512, generator=g) * 0.02
+    host_b = torch.randn(256, 512, generator=g) * 0.02
+    torch.cuda.synchronize()
+    w = host_a.to(cuda)
+    ptr = w.data_ptr()
+    p = conv.get("layer", w)
+    del w
+    reused = None
+    for _ in range(8):  # the caching allocator hands the freed block back
+        w = host_b.to(cuda)
+        if w.data_ptr() == ptr and w._version == 0:
+            reused = w
+            break
+        del w
+    if reused is None:
+        pytest.skip("the allocator did not reuse the freed block")
+    p2 = conv.get("layer", reused)
+    assert conv.prepared == 2 and p2 is not p
+    assert torch.equal(p2.data, w4.pack_uint4(reused, group_size=128).data)

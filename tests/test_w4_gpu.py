@@ -195,6 +195,28 @@ def test_cfg2_decode_full_size(cuda, m):
         check_product(y, y64, absmag, out_dtype, f"cfg2 m{m} {out_dtype}")
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 16])
+@pytest.mark.parametrize("adtype", [torch.bfloat16, torch.float16])
+def test_uint4_decode_row_counts_and_activation_types(cuda, m, adtype):
+    """The uint4 decode path (K 3073-4096, g128, bf16 scales, nk storage) at
+    every row-count instantiation the launcher picks for M <= 16 (1, 2-4, 5-16)
+    and with fp16 as well as bf16 activations; N 2048 keeps it short."""
+    case(f"uint4 decode m{m} {adtype} k4096 n2048")
+    g = torch.Generator().manual_seed(40 + m)
+    w = (torch.randn(2048, 4096, generator=g) * 0.02)
+    a = torch.randn(m, 4096, generator=g).to(adtype)
+    p = w4().pack_uint4(w.to(cuda), group_size=128)
+    r = o4.pack_uint4_baseline(w.numpy(), group_size=128)
+    av = act_values(a)
+    cen = o4.dequant_baseline(r, floating=False)
+    s = bf16_bits_to_f32(r["scales"])
+    y64 = o4.w4a16_linear(av, cen, s, 128)
+    absmag = o4.w4a16_linear(np.abs(av), np.ones_like(cen), s, 128)
+    for out_dtype in (adtype, torch.float32):
+        y = w4().w4a16_gemm(a.to(cuda), p, out_dtype=out_dtype)
+        check_product(y, y64, absmag, out_dtype, f"uint4 decode m{m} {adtype} -> {out_dtype}")
+
+
 @pytest.mark.parametrize("g", o4.GROUPS)
 @pytest.mark.parametrize("layout,order", [("nk", "low"), ("nk", "high"), ("kn", "low")])
 @pytest.mark.parametrize("adtype", [torch.float16, torch.bfloat16])

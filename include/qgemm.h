@@ -140,6 +140,32 @@ int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t m,
                    size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Allocation-free W8A8 linear: qg_w8a8_linear without a workspace argument.
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the workspace is a file-scope device array of
+ * QG_W8A8_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, held until the process
+ * ends; the call makes no hipMalloc / hipFree or other allocation. The caller
+ * still passes inputs and outputs, as for qg_w8a8_linear (same arguments, same
+ * results, bit for bit). Limit: qg_w8a8_linear_workspace_bytes(w, w_sn, m, n, k)
+ * must not exceed QG_W8A8_NOALLOC_SCRATCH_BYTES (cfg1's K = 12288 down
+ * projection at m = 4096 needs 50.3 MB), else hipErrorInvalidValue before any
+ * HIP call. The stream must belong to the current device
+ * (hipErrorInvalidDevice otherwise). Every call on one GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller. The first call on a
+ * device looks up the array's address (hipGetSymbolAddress); make it outside
+ * graph capture.
+ * ------------------------------------------------------------------------- */
+#define QG_W8A8_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int qg_w8a8_linear_noalloc(const void* x, int x_dtype, int64_t x_sm, int64_t m,
+                           int64_t k, const int8_t* w, int64_t w_sn, int64_t n,
+                           const float* w_scale, int64_t w_scale_numel,
+                           const void* bias, int bias_dtype, void* out,
+                           int out_dtype, int rounding, int epilogue,
+                           void* stream);
+
+/* ---------------------------------------------------------------------------
  * INT4 weight storage (W4).
  * A W4 weight [n, k] quantised in groups of G = group_size (32, 64 or 128)
  * consecutive K values per output row n:

@@ -7,6 +7,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "../../include/qgemm.h"
 #include "qg_internal.h"
 
@@ -192,11 +195,15 @@ extern "C" size_t qg_w8a8_linear_workspace_bytes(const int8_t* w, int64_t w_sn, 
   return plan_w8a8(w, w_sn, m, n, k).total();
 }
 
-extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t k,
-                              const int8_t* w, int64_t w_sn, int64_t n, const float* w_scale,
-                              int64_t w_scale_numel, const void* bias, int bias_dtype, void* out,
-                              int out_dtype, int rounding, int epilogue, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+namespace {
+
+// Validation and launches of the W8A8 linear into a given workspace: shared by
+// qg_w8a8_linear (caller workspace) and qg_w8a8_linear_noalloc (the library's
+// scratch array). `capacity` is the workspace size.
+int w8a8_linear_run(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t k, const int8_t* w,
+                    int64_t w_sn, int64_t n, const float* w_scale, int64_t w_scale_numel, const void* bias,
+                    int bias_dtype, void* out, int out_dtype, int rounding, int epilogue, char* ws,
+                    size_t capacity, hipStream_t s) {
   if (m < 0 || n < 0 || k < 0 || k > kMaxK || x_sm < 0 || w_sn < 0) return hipErrorInvalidValue;
   if (m > kIntMax || n > kIntMax || m * n > (int64_t(1) << 40)) return hipErrorInvalidValue;
   if (!float_dtype(x_dtype) || !float_dtype(out_dtype)) return hipErrorInvalidValue;
@@ -207,12 +214,10 @@ extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t 
   if (m == 0 || n == 0) return hipSuccess;
   if (!out || (k > 0 && (!x || !w))) return hipErrorInvalidValue;
   const W8A8Plan pl = plan_w8a8(w, w_sn, m, n, k);
-  if (!workspace || workspace_bytes < pl.total() || !aligned16(workspace)) return hipErrorInvalidValue;
+  if (!ws || capacity < pl.total() || !aligned16(ws)) return hipErrorInvalidValue;
   if (m * pl.kp >= kMaxOperandBytes || n * pl.kp >= kMaxOperandBytes) return hipErrorInvalidValue;
-  char* ws = static_cast<char*>(workspace);
   int8_t* xq = reinterpret_cast<int8_t*>(ws);
   float* xs = reinterpret_cast<float*>(ws + pl.act_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = qg::launch_quant_rows(x, x_dtype, x_sm, 1, m, k, xq, pl.kp, pl.kp, xs, rounding, s);
   if (e != hipSuccess) return e;
   qg::I8GemmArgs p{};
@@ -240,6 +245,88 @@ extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t 
   p.out_dtype = out_dtype;
   p.epi = epilogue;
   return qg::launch_i8_gemm(p, s);
+}
+
+}  // namespace
+
+extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t k,
+                              const int8_t* w, int64_t w_sn, int64_t n, const float* w_scale,
+                              int64_t w_scale_numel, const void* bias, int bias_dtype, void* out,
+                              int out_dtype, int rounding, int epilogue, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  return w8a8_linear_run(x, x_dtype, x_sm, m, k, w, w_sn, n, w_scale, w_scale_numel, bias, bias_dtype, out,
+                         out_dtype, rounding, epilogue, static_cast<char*>(workspace), workspace_bytes,
+                         static_cast<hipStream_t>(stream));
+}
+
+// --------------------------------------------------------------------------
+// Allocation-free W8A8 linear. Its workspace (the int8 activations, their
+// steps and a packed weight when the weight is not canonical) lives in this
+// file-scope device array: one copy per GPU, at its own address on each, held
+// until the process ends. Every byte a call reads from it is written by the
+// same call first (the quantizer writes the K padding, the packer whole padded
+// rows), so nothing has to be cleared between calls; calls that overlap in time
+// on one GPU share the array and race.
+namespace {
+
+static __device__ __align__(256) char scratch[QG_W8A8_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<char*> g_scratch_addr[kMaxScratchDevices];
+std::mutex g_scratch_lock;
+
+// The device address of `scratch` on `device`, looked up once per device with
+// that device current (host code never passes the array's own name: on the
+// host it is a stand-in symbol, not a device address).
+hipError_t scratch_address(int device, char** addr) {
+  if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  char* p = g_scratch_addr[device].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    p = g_scratch_addr[device].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      int current = -1;
+      hipError_t e = hipGetDevice(&current);
+      if (e != hipSuccess) return e;
+      if (current != device) return hipErrorInvalidDevice;
+      void* sym = nullptr;
+      e = hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return e;
+      if (sym == nullptr) return hipErrorInvalidSymbol;
+      p = static_cast<char*>(sym);
+      g_scratch_addr[device].store(p, std::memory_order_release);
+    }
+  }
+  *addr = p;
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int qg_w8a8_linear_noalloc(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t k,
+                                      const int8_t* w, int64_t w_sn, int64_t n, const float* w_scale,
+                                      int64_t w_scale_numel, const void* bias, int bias_dtype, void* out,
+                                      int out_dtype, int rounding, int epilogue, void* stream) {
+  // argument errors before any HIP call (the workspace check needs the plan)
+  if (m < 0 || n < 0 || k < 0 || k > kMaxK || w_sn < 0) return hipErrorInvalidValue;
+  if (m == 0 || n == 0) return hipSuccess;
+  if (plan_w8a8(w, w_sn, m, n, k).total() > QG_W8A8_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
+  // the scratch of the device the stream runs on, which must be the current one
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int device = -1;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  if (s != nullptr) {
+    hipDevice_t stream_device = -1;
+    e = hipStreamGetDevice(s, &stream_device);
+    if (e != hipSuccess) return e;
+    if (stream_device != device) return hipErrorInvalidDevice;
+  }
+  char* ws = nullptr;
+  e = scratch_address(device, &ws);
+  if (e != hipSuccess) return e;
+  return w8a8_linear_run(x, x_dtype, x_sm, m, k, w, w_sn, n, w_scale, w_scale_numel, bias, bias_dtype, out,
+                         out_dtype, rounding, epilogue, ws, QG_W8A8_NOALLOC_SCRATCH_BYTES, s);
 }
 
 // --------------------------------------------------------------------------

@@ -58,6 +58,8 @@ SIGNATURES = {
     "qg_w8a8_linear_workspace_bytes": (_sz, [_p, _i64, _i64, _i64, _i64]),
     "qg_w8a8_linear": (_i, [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _i, _p, _i, _i,
                             _i, _p, _sz, _p]),
+    "qg_w8a8_linear_noalloc": (_i, [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _i, _p, _i, _i,
+                                    _i, _p]),
     "qg_w4_pack": (_i, [_p, _i, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _p, _i, _p, _p, _p]),
     "qg_w4_unpack": (_i, [_p, _i64, _i64, _i, _i, _p, _i, _p, _p, _i, _p]),
     "qg_w4a16_gemm_workspace_bytes": (_sz, [_i64, _i64, _i64, _i, _i]),

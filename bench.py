@@ -277,7 +277,8 @@ class DecodeW4:
 
     @staticmethod
     def kernel_name(m):
-        return "k_w4_decode<RP=1,CT=2,G=128,uint4>" if m == 1 else "k_w4_decode<RP=16,CT=4,G=128,uint4>"
+        return ("k_w4_gemv1 (one row: 32 columns x 8 waves, global->LDS copies, 16x16x32 bf16 MFMA)" if m == 1
+                else "k_w4_decode<RP=16,CT=4,G=128,uint4>")
 
 
 def run_w4a16(torch, lib, _lib, dev, rows=(1, 16, 2048), copies=12):

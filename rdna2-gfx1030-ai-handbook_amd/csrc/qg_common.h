@@ -125,6 +125,21 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
       : "memory");
 }
 
+// 4-byte variant (global_load_lds_dword): lane i writes bytes
+// [lds_addr + 4 i, lds_addr + 4 i + 4); lanes outside the exec mask write nothing.
+__device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(sbase)
+      : "memory");
+}
+
 // Wait until at most N vector-memory operations of this wave are in flight
 // (loads complete in order), drain LDS reads, then barrier the workgroup.
 template <int N>

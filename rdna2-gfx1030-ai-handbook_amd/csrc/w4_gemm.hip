@@ -793,6 +793,130 @@ hipError_t launch_skinny_t(const W4Args& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Single-row W4A16 decode (M = 1) on the BASELINE uint4 storage: unsigned
+// nibbles, low order, [N, K/8] words, bf16 scales, packed uint4 zero points,
+// group 128, bf16 activations, K a multiple of 512 up to 4096.
+//
+// Workgroup = 32 columns (n0 = 32 b), 8 waves; wave w owns K range
+// [512 w, 512 w + 512) (groups 4 w .. 4 w + 3) of all 32 columns. Every
+// operand reaches LDS by direct global -> LDS copies issued at the start
+// (nothing else is in flight, so the waits are exact vmcnt counts):
+//   activations  the wave's 512 values (1 KB), then reordered in place to
+//                (0 2 4 6 1 3 5 7) per 8 for the 7-op nibble unpack;
+//   scales       8 B per column (groups 4 w .. 4 w + 3), one 4-byte copy per lane;
+//   zero points  the packed word holding those groups, lanes 0-31;
+//   weights      8 copies of 4 columns x 256 B (two whole cache lines per
+//                column): copy i, lane L lands in 16-byte slot 64 i + L =
+//                c * 16 + (k ^ (c & 14)), c = 4 i + L / 16 the local column and
+//                k the 16-byte chunk of its 256 B. The XOR makes the MFMA-layout
+//                reads below (lane (col, q) -> chunk 4 g + q of column col)
+//                hit distinct banks for each group of 32 lanes.
+// Columns 0-15 (copies 0-3) are computed while columns 16-31 still arrive.
+// Per group g: v_mfma_f32_16x16x32_bf16 of the activations (A, all 16 rows
+// the same vector) with 128 + u (B, exact bf16), plus one MFMA against ones
+// for the group's activation sum; y += s (acc - (128 + z) sum) in fp32. The 8
+// waves' partial columns are summed through LDS in wave order.
+constexpr int kGemv1Region = 8192 + 1024 + 256 + 128;  // LDS bytes per wave
+constexpr int kGemv1Lds = 8 * kGemv1Region + 8 * 32 * 4;
+
+__global__ __launch_bounds__(512) void k_w4_gemv1(W4Args p) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(1024))) char smem[kGemv1Lds];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * 32;
+  const bool live = 512 * wave < p.K;  // waves past K contribute zero
+  char* const region = smem + wave * kGemv1Region;
+  char* const wt = region;             // weights, 32 columns x 256 B
+  char* const at = region + 8192;      // activations, 512 bf16
+  char* const st = region + 9216;      // scales [column][4] bf16
+  char* const zt = region + 9472;      // zero-point words [column]
+  float total[2] = {0.0f, 0.0f};
+  if (live) {
+    const int KW = p.K >> 3;
+    dma16s(p.a, 1024u * wave + 16u * lane, lds_addr_of(at));
+    {
+      const int c = min(n0 + (lane >> 1), p.N - 1);
+      dma4s(p.scales, 2u * (static_cast<uint32_t>(c) * p.ng + 4 * wave) + 4u * (lane & 1), lds_addr_of(st));
+    }
+    if (lane < 32) {
+      const int c = min(n0 + lane, p.N - 1);
+      dma4s(p.zeros, 4u * (static_cast<uint32_t>(c) * p.zw + (wave >> 1)), lds_addr_of(zt));
+    }
+    static_for<0, 8>([&](auto i) {
+      const int c = 4 * i + (lane >> 4);
+      const int k = (lane & 15) ^ (c & 14);
+      const int n = min(n0 + c, p.N - 1);
+      dma16s(p.w, 4u * (static_cast<uint32_t>(n) * KW + 64 * wave + 4 * k), lds_addr_of(wt + 1024 * i));
+    });
+    wait_vm<8>();  // activations, scales, zero points (the 8 weight copies may fly)
+    {
+      char* const a16 = at + 16 * lane;
+      *reinterpret_cast<i32x4*>(a16) = even_odd(*reinterpret_cast<const i32x4*>(a16));
+    }
+    const int col = lane & 15, q = lane >> 4;
+    Unpack7<false, true> unpack;
+    unpack.init(false);
+    uint32_t ones2 = 0x3F803F80u;  // bf16 (1, 1)
+    asm volatile("" : "+v"(ones2));
+    const i32x4 ones = {static_cast<int>(ones2), static_cast<int>(ones2), static_cast<int>(ones2),
+                        static_cast<int>(ones2)};
+    // activation sums of the wave's 4 groups (column independent)
+    f32x4 asum[4];
+    static_for<0, 4>([&](auto g) {
+      asum[g] = f32x4{0, 0, 0, 0};
+      static_for<0, 4>([&](auto j) {
+        const i32x4 af = *reinterpret_cast<const i32x4*>(at + 2 * (128 * g + 32 * q + 8 * j));
+        asum[g] = mfma16<false>(af, ones, asum[g]);
+      });
+    });
+    static_for<0, 2>([&](auto t) {
+      if constexpr (t == 0) wait_vm<4>();
+      else wait_vm<0>();
+      const int c = 16 * t + col;
+      const uint32_t zword = *reinterpret_cast<const uint32_t*>(zt + 4 * c) >> (16 * (wave & 1));
+      static_for<0, 4>([&](auto g) {
+        const int k = 4 * g + q;
+        const i32x4 wv = *reinterpret_cast<const i32x4*>(wt + 16 * (c * 16 + (k ^ (c & 14))));
+        f32x4 acc = {0, 0, 0, 0};
+        static_for<0, 4>([&](auto j) {
+          const i32x4 af = *reinterpret_cast<const i32x4*>(at + 2 * (128 * g + 32 * q + 8 * j));
+          acc = mfma16<false>(af, unpack(static_cast<uint32_t>(wv[int(j)])), acc);
+        });
+        const float s = bf16_to_f32(*reinterpret_cast<const uint16_t*>(st + 8 * c + 2 * g));
+        const float zb = 128.0f + static_cast<float>((zword >> (4 * g)) & 15u);
+        total[t] = __builtin_fmaf(s, __builtin_fmaf(-zb, asum[g][0], acc[0]), total[t]);
+      });
+    });
+  }
+  // ---- partial columns of the 8 waves (row 0 sits in lanes 0-15, register 0)
+  float* red = reinterpret_cast<float*>(smem + 8 * kGemv1Region);
+  if (lane < 16) {
+    red[wave * 32 + lane] = total[0];
+    red[wave * 32 + 16 + lane] = total[1];
+  }
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    float v = red[threadIdx.x];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) v = v + red[w * 32 + threadIdx.x];
+    const int n = n0 + threadIdx.x;
+    if (n < p.N) {
+      if (p.bias) v = v + load_bias(p.bias, p.bias_dtype, n);
+      store_out(p.out, p.out_dtype, n, v);
+    }
+  }
+}
+
+// The single-row kernel's operand contract (see k_w4_gemv1).
+bool gemv1_applies(const W4Args& p) {
+  const uintptr_t align = reinterpret_cast<uintptr_t>(p.w) | reinterpret_cast<uintptr_t>(p.a);
+  return p.M == 1 && !p.a_f16 && p.group == 128 && !p.scale_f32 && p.flags == QG_W4_ZEROS_PACKED &&
+         p.K % 512 == 0 && p.K <= 4096 && (align & 15) == 0 &&
+         ((reinterpret_cast<uintptr_t>(p.scales) | reinterpret_cast<uintptr_t>(p.zeros)) & 3) == 0;
+}
+
 template <int FM, int CT, bool F16A>
 hipError_t launch_skinny_g(const W4Args& p, hipStream_t stream) {
   const bool kn = p.flags & QG_W4_LAYOUT_KN;
@@ -841,7 +965,13 @@ hipError_t launch_skinny(const W4Args& p, hipStream_t stream) {
     // two for 1-4 rows (cfg2, 448 workgroups: 2-4 rows 9.5-9.7 us against
     // 10.0-10.1 us with four), four for 5-16 rows (11.2-11.4 us against 12.9 us
     // with two)
-    if (p.M == 1) return launch_decode_g<1, 2, F16A>(p, stream);
+    if (p.M == 1) {
+      if (gemv1_applies(p)) {
+        hipLaunchKernelGGL(k_w4_gemv1, dim3(ceil_div(p.N, 32)), dim3(512), 0, stream, p);
+        return hipGetLastError();
+      }
+      return launch_decode_g<1, 2, F16A>(p, stream);
+    }
     if (p.M <= 4) return launch_decode_g<4, 2, F16A>(p, stream);
     return launch_decode_g<16, 4, F16A>(p, stream);
   }

@@ -247,6 +247,19 @@ def unpack_int4(p, *, dtype=torch.float16):
     return out
 
 
+def _gemv1_applies(a, p):
+    """Whether the C ABI serves this call with the single-row kernel
+    (k_w4_gemv1): one bf16 activation row, the BASELINE uint4 storage (nk, low
+    order, bf16 scales, packed zero points), group 128, K a multiple of 512 up
+    to 4096, 16-byte aligned weights and activations."""
+    a = a if (a.stride(1) == 1 and a.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0) else a.contiguous()
+    return (a.shape[0] == 1 and a.dtype == torch.bfloat16 and p.group_size == 128
+            and p.flags == _lib.W4_ZEROS_PACKED and p.scales.dtype == torch.bfloat16
+            and p.k % 512 == 0 and p.k <= 4096
+            and p.data.data_ptr() % 16 == 0 and a.data_ptr() % 16 == 0
+            and p.scales.data_ptr() % 4 == 0 and p.zeros.data_ptr() % 4 == 0)
+
+
 def w4a16_gemm(a, p, bias=None, *, out_dtype=None):
     """The fused W4A16 kernel: out = a @ dequant(p)^T (+ bias), fp32
     accumulation, one rounding to out_dtype (default: a's dtype)."""
@@ -302,9 +315,13 @@ def int4_linear_a16(a, p, *, bias=None, method="dequant", prepared=None, tile=(6
         if m > 64 and p.k % 128 == 0:
             return out, _lib.kernel_metadata("w4a16_tiled_mfma", (128, 128, 128), "k_wd_gemm")
         if m <= 16 and -(-p.k // 128) <= 32:
+            if _gemv1_applies(a, p):
+                return out, _lib.kernel_metadata("w4a16_gemv1", (1, 32, 512), "k_w4_gemv1")
             rp = 1 if m == 1 else 4 if m <= 4 else 16
-            cols = 64 if rp == 16 else 32
-            return out, _lib.kernel_metadata("w4a16_decode", (rp, cols, 128), "k_w4_decodeILi{}E".format(rp))
+            # column tiles of 16 per workgroup, as launch_decode_g picks them
+            ct = (4 if rp == 16 else 2) if p.group_size == 128 else 2 if p.group_size == 64 else (1 if rp > 1 else 2)
+            return out, _lib.kernel_metadata("w4a16_decode", (rp, 16 * ct, 128),
+                                             "k_w4_decodeILi{}ELi{}ELi{}E".format(rp, ct, p.group_size))
         fm = 1 if m <= 16 else 2 if m <= 32 else 4
         return out, _lib.kernel_metadata("w4a16_skinny", (16 * fm, 16, 128), "k_w4_skinnyILi{}E".format(fm))
     return out

@@ -195,6 +195,45 @@ def test_cfg2_decode_full_size(cuda, m):
         check_product(y, y64, absmag, out_dtype, f"cfg2 m{m} {out_dtype}")
 
 
+@pytest.mark.parametrize("n,k", [(1000, 512), (4100, 1536), (64, 4096), (14336, 4096)])
+def test_uint4_single_row_kernel(cuda, n, k):
+    """The single-row kernel (one bf16 row, uint4 storage, g128, K a multiple
+    of 512 up to 4096): ragged N, short K (waves past K idle), bias and every
+    output dtype, against the float64 oracle; and the kernel metadata names it."""
+    case(f"uint4 single-row kernel n{n} k{k}")
+    g = torch.Generator().manual_seed(n + k)
+    w = torch.randn(n, k, generator=g) * 0.02
+    a = torch.randn(1, k, generator=g).to(torch.bfloat16)
+    b = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16)
+    p = w4().pack_uint4(w.to(cuda), group_size=128)
+    r = o4.pack_uint4_baseline(w.numpy(), group_size=128)
+    av = act_values(a)
+    cen = o4.dequant_baseline(r, floating=False)
+    s = bf16_bits_to_f32(r["scales"])
+    absmag = o4.w4a16_linear(np.abs(av), np.ones_like(cen), s, 128)
+    for bias in (None, b):
+        y64 = o4.w4a16_linear(av, cen, s, 128, None if bias is None else act_values(bias))
+        for out_dtype in (torch.bfloat16, torch.float16, torch.float32):
+            y = w4().w4a16_gemm(a.to(cuda), p, None if bias is None else bias.to(cuda), out_dtype=out_dtype)
+            check_product(y, y64, absmag, out_dtype, f"single-row n{n} k{k} bias={bias is not None} {out_dtype}")
+    _, md = w4().int4_linear_a16(a.to(cuda), p, method="dot2", return_kernel=True)
+    assert md["variant"] == "w4a16_gemv1" and md["vgpr"] is not None
+
+
+def test_decode_metadata_column_tiles(cuda):
+    """The decode kernel's reported column tile follows the launcher's choice
+    per group size and row count (16 * CT columns)."""
+    case("decode metadata column tiles")
+    g = torch.Generator().manual_seed(9)
+    for group, m, cols in ((32, 1, 32), (32, 5, 16), (64, 5, 32), (128, 5, 64), (128, 3, 32)):
+        w = torch.randn(96, 512, generator=g) * 0.02
+        p = w4().pack_int4(w.to(cuda), group_size=group, symmetric=False)
+        a = torch.randn(m, 512, generator=g).to(torch.float16).to(cuda)
+        _, md = w4().int4_linear_a16(a, p, method="dot2", return_kernel=True)
+        assert md["variant"] == "w4a16_decode" and md["tile"][1] == cols, (group, m, md)
+        assert md["vgpr"] is not None, (group, m)
+
+
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 16])
 @pytest.mark.parametrize("adtype", [torch.bfloat16, torch.float16])
 def test_uint4_decode_row_counts_and_activation_types(cuda, m, adtype):

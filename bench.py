@@ -304,9 +304,12 @@ def run_w4a16(torch, lib, _lib, dev, rows=(1, 16, 2048), copies=12):
         y = torch.empty(m, N, dtype=torch.bfloat16, device=dev)
         P = _lib.ptr
 
+        wsb = int(lib.qg_w4a16_gemm_workspace_bytes(m, N, K, G, p0.flags))
+        ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+
         def call(i, stream):
             _lib.check(lib.qg_w4a16_gemm(P(a), _lib.BF16, K, m, K, P(p0.data), N, G, p0.flags, P(p0.scales),
-                                         _lib.BF16, P(p0.zeros), None, 0, P(y), _lib.BF16, None, 0, stream),
+                                         _lib.BF16, P(p0.zeros), None, 0, P(y), _lib.BF16, P(ws), wsb, stream),
                        "w4a16")
         ms = statistics.median([_graph_time(torch, call, 10, replays=2) for _ in range(3)])
         bytes_ = wbytes + m * K * 2 + m * N * 2

@@ -214,14 +214,19 @@ int qg_w4_unpack(const int32_t* data, int64_t n, int64_t k, int group_size,
  * W4A16 linear: out[m, n] = sum_k a[m, k] * ((q[n,k] - zero[n,g]) * scale[n,g])
  * (+ bias[n]), fp32 accumulation, one rounding to out_dtype.
  * Replaces: int4_linear_a16 (int4_weight_gemm_v07.py:540-564) with its
- *   _linear_dot2 kernel (:365-387); the reference rounds every dequantised
- *   weight to fp16 first, this library applies each group scale to the exact
- *   group partial sum instead (closer to the exact product).
+ *   _linear_dot2 kernel (:365-387) and its default dequant method (:549-554).
+ * Decode shapes and smaller prefill grids apply each group scale to the exact
+ * group partial sum (closer to the exact product than the reference, which
+ * rounds every dequantised weight to fp16 first). Prefill grids of more than
+ * 64 rows and >= 192 output tiles of 256 x 192 (K a multiple of 64) take the
+ * reference's dequant formulation instead: W is dequantised once into the
+ * workspace, (q - z) * s in fp32 rounded to the activation dtype, then a
+ * 2-byte MFMA GEMM with fp32 accumulation runs on it; the workspace is then
+ * 2 * n * k bytes (16-byte aligned), reported by
+ * qg_w4a16_gemm_workspace_bytes (0 on the other shapes), and required.
  * a: [m, k] QG_F16 or QG_BF16, unit K stride, row stride a_sm (a multiple of 8
  * elements, 16-byte aligned base); w: 16-byte aligned; out: [m, n] contiguous
- * QG_F16 / QG_BF16 / QG_F32; bias NULL or [n] of bias_dtype; m * n < 2^31.
- * The workspace is currently unused (qg_w4a16_gemm_workspace_bytes returns 0);
- * it is part of the signature so that split-K variants keep the ABI. */
+ * QG_F16 / QG_BF16 / QG_F32; bias NULL or [n] of bias_dtype; m * n < 2^31. */
 size_t qg_w4a16_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int group_size,
                                      int flags);
 int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m, int64_t k,

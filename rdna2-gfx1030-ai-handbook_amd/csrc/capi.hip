@@ -395,14 +395,27 @@ extern "C" int qg_w4_unpack(const int32_t* data, int64_t n, int64_t k, int group
   return qg::launch_w4_unpack(p, static_cast<hipStream_t>(stream));
 }
 
+namespace {
+
+// Large prefill grids (more than kW4TiledMinRows rows, >= 192 tiles of
+// 256 x 192 — the INT8 kernel's large-grid rule — and K a multiple of the
+// 64-element stage): W is dequantised once into the workspace as the
+// activation dtype, (q - z) * s in fp32 rounded once (the reference's dequant
+// method, int4_weight_gemm_v07.py:549-554), then the 2-byte ping-pong GEMM
+// runs on it. Returns the workspace bytes (0: the fused tiled kernel).
+size_t w4_prefill_bytes(int64_t m, int64_t n, int64_t k) {
+  const int64_t tiles = ((m + 255) / 256) * ((n + 191) / 192);
+  if (m <= kW4TiledMinRows || k % 64 != 0 || tiles < 192) return 0;
+  if (2 * n * k >= kMaxOperandBytes) return 0;
+  return static_cast<size_t>(round_up(2 * n * k, 256));
+}
+
+}  // namespace
+
 extern "C" size_t qg_w4a16_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int group_size,
                                                 int flags) {
-  (void)m;
-  (void)n;
-  (void)k;
-  (void)group_size;
-  (void)flags;
-  return 0;
+  if (!valid_w4_shape(n, k, group_size, flags) || m < 0 || m > kIntMax) return 0;
+  return w4_prefill_bytes(m, n, k);
 }
 
 extern "C" int qg_w4a8_gemm(const int8_t* a, int64_t a_sm, int64_t m, int64_t k, const int32_t* w, int64_t n,
@@ -455,8 +468,6 @@ extern "C" int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m
                              const void* scales, int scales_dtype, const void* zeros,
                              const void* bias, int bias_dtype, void* out, int out_dtype,
                              void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (!valid_w4_shape(n, k, group_size, flags)) return hipErrorInvalidValue;
   if (m < 0 || m > kIntMax || m * n >= (int64_t(1) << 31)) return hipErrorInvalidValue;
   if (a_dtype != QG_F16 && a_dtype != QG_BF16) return hipErrorInvalidValue;
@@ -488,6 +499,35 @@ extern "C" int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m
   p.bias_dtype = bias_dtype;
   p.out = out;
   p.out_dtype = out_dtype;
+  // large prefill grids: dequantise W into the workspace, then the 2-byte
+  // ping-pong GEMM (out = acc + bias, one rounding)
+  const size_t need = w4_prefill_bytes(m, n, k);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need || !aligned16(workspace)) return hipErrorInvalidValue;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    qg::W4Args u = p;
+    u.out = workspace;
+    u.out_dtype = a_dtype;
+    hipError_t e = qg::launch_w4_unpack(u, s);
+    if (e != hipSuccess) return e;
+    qg::I8GemmArgs g{};
+    g.a = static_cast<const int8_t*>(a);
+    g.a_sm = a_sm;
+    g.w = static_cast<const int8_t*>(workspace);
+    g.w_sn = k;
+    g.M = p.M;
+    g.N = p.N;
+    g.K = p.K;
+    g.a_scale = nullptr;
+    g.b_scale = nullptr;
+    g.b_scalar = 0;
+    g.bias = bias;
+    g.bias_dtype = bias_dtype;
+    g.out = out;
+    g.out_dtype = out_dtype;
+    g.epi = 0;
+    return qg::launch_h16_gemm(g, p.a_f16 != 0, s);
+  }
   // large M: the tiled kernel (activation rows staged in LDS, 128-wide K stages)
   if (m > kW4TiledMinRows && k % 128 == 0) {
     qg::WdArgs t{};

@@ -312,6 +312,10 @@ def int4_linear_a16(a, p, *, bias=None, method="dequant", prepared=None, tile=(6
         # the C ABI's choice: the tiled MFMA kernel past 64 rows (K a multiple of
         # 128), the decode kernel for up to 16 rows and K <= 4096, else skinny
         m = a.shape[0]
+        if _lib.library().qg_w4a16_gemm_workspace_bytes(m, p.n, p.k, p.group_size, p.flags) > 0:
+            # large prefill grid: W dequantised into the workspace, then the
+            # 2-byte ping-pong GEMM (256 x 192 tiles, K stage of 64 elements)
+            return out, _lib.kernel_metadata("w4a16_dequant_pingpong", (256, 192, 64), "k_h16_gemm_pp")
         if m > 64 and p.k % 128 == 0:
             return out, _lib.kernel_metadata("w4a16_tiled_mfma", (128, 128, 128), "k_wd_gemm")
         if m <= 16 and -(-p.k // 128) <= 32:

@@ -160,4 +160,6 @@ def kernel_metadata(variant: str, tile, symbol_hint: str) -> dict:
             "vgpr": res.get("VGPRs"), "agpr": res.get("AGPRs"), "sgpr": res.get("TotalSGPRs"),
             "lds_bytes": res.get("LDS Size [bytes/block]"), "scratch_bytes": res.get("ScratchSize [bytes/lane]"),
             "spills": (res.get("VGPRs Spill") or 0) + (res.get("SGPRs Spill") or 0) if res else None,
+            # SGPR spills go to VGPR lanes (v_writelane), VGPR spills to scratch memory
+            "vgpr_spills": res.get("VGPRs Spill"), "sgpr_spills": res.get("SGPRs Spill"),
             "occupancy_waves_per_simd": res.get("Occupancy [waves/SIMD]"), "symbol": symbol_hint}

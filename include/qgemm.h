@@ -140,6 +140,52 @@ int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t m,
                    size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * ConvRot prologue: per-row INT8 quantization after rotating every group of
+ * rot_group consecutive K values by the normalised Hadamard matrix
+ * H / sqrt(rot_group) (Sylvester order, H[i][j] = (-1)^popcount(i & j)).
+ * Replaces, as an opt-in fused path: Kitchen's _build_hadamard +
+ *   _rotate_activation + quantize_int8_rowwise of the MOSS linear
+ *   (rdna2-ops/rdna2_ops/comfy_int8.py:112-122; every MOSS call uses
+ *   convrot=True, convrot_groupsize=256). Kitchen rotates with a dense fp32
+ *   matmul; this library uses the fast Walsh-Hadamard butterflies, which form
+ *   the same sums in another order (agreement to a few fp32 ulps, so codes can
+ *   differ by 1 where the quotient is within a few ulps of a rounding tie).
+ * x: [m, k] QG_F32 / QG_F16 / QG_BF16, unit K stride, row stride x_sm >= k;
+ * rot_group a power of two in [2, 1024] dividing k; k <= QG_ROT_MAX_K.
+ * q [m, k] (row stride q_sm >= k), step [m]: as qg_quant_rows_i8 on the
+ * rotated rows.
+ * ------------------------------------------------------------------------- */
+#define QG_ROT_MAX_K 16384
+int qg_rot_quant_rows_i8(const void* x, int x_dtype, int64_t x_sm, int64_t m,
+                         int64_t k, int rot_group, int8_t* q, int64_t q_sm,
+                         float* step, int rounding, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * W8A8 linear with the opt-in MOSS fusion: qg_w8a8_linear plus an optional
+ * ConvRot prologue (rot_group > 0, see qg_rot_quant_rows_i8) and an optional
+ * residual epilogue term.
+ * Replaces, as an opt-in fused path: the MOSS int8_linear body
+ *   (rdna2-ops/rdna2_ops/comfy_int8.py:98-145: ConvRot, quantizer, GEMM,
+ *   scaling, bias, Kitchen's _apply_residual).
+ * residual: NULL or [m, n] (row stride residual_sm >= n) of residual_dtype
+ * (QG_F32 / QG_F16 / QG_BF16); residual_scale: NULL, one value or [n] fp32.
+ * The epilogue adds f32(residual) (* residual_scale) in fp32 after the scale,
+ * bias and activation steps and before the single rounding to out_dtype, so
+ * fp32 outputs equal the fp32 sequence scale -> + bias -> + residual bit for
+ * bit. Not with QG_EPI_ORDER_EAGER. The workspace is that of qg_w8a8_linear
+ * (qg_w8a8_linear_workspace_bytes).
+ * ------------------------------------------------------------------------- */
+int qg_w8a8_linear_ex(const void* x, int x_dtype, int64_t x_sm, int64_t m,
+                      int64_t k, const int8_t* w, int64_t w_sn, int64_t n,
+                      const float* w_scale, int64_t w_scale_numel,
+                      const void* bias, int bias_dtype, int rot_group,
+                      const void* residual, int residual_dtype,
+                      int64_t residual_sm, const float* residual_scale,
+                      int64_t residual_scale_numel, void* out, int out_dtype,
+                      int rounding, int epilogue, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Allocation-free W8A8 linear: qg_w8a8_linear without a workspace argument.
  * No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

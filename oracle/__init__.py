@@ -16,5 +16,10 @@ How each function is pinned (see tests/test_oracle_*.py):
   int8.quant_rows        exact ties (x/step = k + 1/2) for both rounding rules,
                          torch CPU division + round, zero rows, clamp.
   int8.gelu_tanh         torch CPU F.gelu(approximate="tanh") to <= 1 fp32 ulp class.
+  convrot.*              Sylvester recursion and scipy.linalg.hadamard, H H^T = g I,
+                         Parseval / involution / e_0 closed forms, the exact float64
+                         rotation within the fp32 error bound, exact small-integer
+                         cases, planted wrong variants, torch CPU fp32 in Kitchen's
+                         order for the residual epilogue.
   int4.*, fp8.*          see their module headers.
 """

@@ -89,6 +89,24 @@ extern "C" int qg_quant_rows_i8(const void* x, int x_dtype, int64_t x_sm, int64_
                                static_cast<hipStream_t>(stream));
 }
 
+namespace {
+bool valid_rot_group(int g, int64_t k) {
+  return g >= 2 && g <= 1024 && (g & (g - 1)) == 0 && k % g == 0 && k <= QG_ROT_MAX_K;
+}
+}  // namespace
+
+extern "C" int qg_rot_quant_rows_i8(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t k,
+                                    int rot_group, int8_t* q, int64_t q_sm, float* step, int rounding,
+                                    void* stream) {
+  if (m < 0 || k < 1 || m > kIntMax || x_sm < k || q_sm < k) return hipErrorInvalidValue;
+  if (!float_dtype(x_dtype) || !valid_rot_group(rot_group, k)) return hipErrorInvalidValue;
+  if (rounding != QG_ROUND_HALF_EVEN && rounding != QG_ROUND_HALF_AWAY) return hipErrorInvalidValue;
+  if (m == 0) return hipSuccess;
+  if (!x || !q || !step) return hipErrorInvalidValue;
+  return qg::launch_rot_quant_rows(x, x_dtype, x_sm, m, k, rot_group, q, q_sm, k, step, rounding,
+                                   static_cast<hipStream_t>(stream));
+}
+
 extern "C" size_t qg_int8_gemm_workspace_bytes(const void* a, int64_t a_sm, int64_t a_sk,
                                                const void* b, int64_t b_sk, int64_t b_sn,
                                                int64_t m, int64_t n, int64_t k) {
@@ -200,11 +218,29 @@ namespace {
 // Validation and launches of the W8A8 linear into a given workspace: shared by
 // qg_w8a8_linear (caller workspace) and qg_w8a8_linear_noalloc (the library's
 // scratch array). `capacity` is the workspace size.
+// Optional ConvRot rotation / residual term (qg_w8a8_linear_ex): rot_group 0 =
+// no rotation; residual nullptr = no residual term.
+struct W8A8Extra {
+  int rot_group = 0;
+  const void* residual = nullptr;
+  int residual_dtype = 0;
+  int64_t residual_sm = 0;
+  const float* residual_scale = nullptr;
+  int64_t residual_scale_numel = 0;
+};
+
 int w8a8_linear_run(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t k, const int8_t* w,
                     int64_t w_sn, int64_t n, const float* w_scale, int64_t w_scale_numel, const void* bias,
                     int bias_dtype, void* out, int out_dtype, int rounding, int epilogue, char* ws,
-                    size_t capacity, hipStream_t s) {
+                    size_t capacity, hipStream_t s, const W8A8Extra& ex = W8A8Extra{}) {
   if (m < 0 || n < 0 || k < 0 || k > kMaxK || x_sm < 0 || w_sn < 0) return hipErrorInvalidValue;
+  if (ex.rot_group != 0 && (!valid_rot_group(ex.rot_group, k) || x_sm < k)) return hipErrorInvalidValue;
+  if (ex.residual) {
+    if (!float_dtype(ex.residual_dtype) || ex.residual_sm < n || (epilogue & QG_EPI_ORDER_EAGER))
+      return hipErrorInvalidValue;
+    if (ex.residual_scale && ex.residual_scale_numel != 1 && ex.residual_scale_numel != n)
+      return hipErrorInvalidValue;
+  }
   if (m > kIntMax || n > kIntMax || m * n > (int64_t(1) << 40)) return hipErrorInvalidValue;
   if (!float_dtype(x_dtype) || !float_dtype(out_dtype)) return hipErrorInvalidValue;
   if (rounding != QG_ROUND_HALF_EVEN && rounding != QG_ROUND_HALF_AWAY) return hipErrorInvalidValue;
@@ -218,9 +254,17 @@ int w8a8_linear_run(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t
   if (m * pl.kp >= kMaxOperandBytes || n * pl.kp >= kMaxOperandBytes) return hipErrorInvalidValue;
   int8_t* xq = reinterpret_cast<int8_t*>(ws);
   float* xs = reinterpret_cast<float*>(ws + pl.act_bytes);
-  hipError_t e = qg::launch_quant_rows(x, x_dtype, x_sm, 1, m, k, xq, pl.kp, pl.kp, xs, rounding, s);
+  hipError_t e = ex.rot_group
+                     ? qg::launch_rot_quant_rows(x, x_dtype, x_sm, m, k, ex.rot_group, xq, pl.kp, pl.kp, xs,
+                                                 rounding, s)
+                     : qg::launch_quant_rows(x, x_dtype, x_sm, 1, m, k, xq, pl.kp, pl.kp, xs, rounding, s);
   if (e != hipSuccess) return e;
   qg::I8GemmArgs p{};
+  p.residual = ex.residual;
+  p.residual_dtype = ex.residual_dtype;
+  p.residual_sm = ex.residual_sm;
+  p.residual_scale = ex.residual_scale;
+  p.residual_scalar = ex.residual_scale_numel == 1;
   p.M = static_cast<int>(m);
   p.N = static_cast<int>(n);
   p.K = static_cast<int>(pl.kp);
@@ -257,6 +301,25 @@ extern "C" int qg_w8a8_linear(const void* x, int x_dtype, int64_t x_sm, int64_t 
   return w8a8_linear_run(x, x_dtype, x_sm, m, k, w, w_sn, n, w_scale, w_scale_numel, bias, bias_dtype, out,
                          out_dtype, rounding, epilogue, static_cast<char*>(workspace), workspace_bytes,
                          static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qg_w8a8_linear_ex(const void* x, int x_dtype, int64_t x_sm, int64_t m, int64_t k,
+                                 const int8_t* w, int64_t w_sn, int64_t n, const float* w_scale,
+                                 int64_t w_scale_numel, const void* bias, int bias_dtype, int rot_group,
+                                 const void* residual, int residual_dtype, int64_t residual_sm,
+                                 const float* residual_scale, int64_t residual_scale_numel, void* out,
+                                 int out_dtype, int rounding, int epilogue, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  W8A8Extra ex;
+  ex.rot_group = rot_group;
+  ex.residual = residual;
+  ex.residual_dtype = residual_dtype;
+  ex.residual_sm = residual_sm;
+  ex.residual_scale = residual_scale;
+  ex.residual_scale_numel = residual_scale_numel;
+  return w8a8_linear_run(x, x_dtype, x_sm, m, k, w, w_sn, n, w_scale, w_scale_numel, bias, bias_dtype, out,
+                         out_dtype, rounding, epilogue, static_cast<char*>(workspace), workspace_bytes,
+                         static_cast<hipStream_t>(stream), ex);
 }
 
 // --------------------------------------------------------------------------

@@ -171,6 +171,30 @@ __device__ __forceinline__ uint32_t epi_bits(int32_t acc, float sa, float sb, fl
   }
 }
 
+// The residual term of output element (row, col) (p.residual non-null).
+__device__ __forceinline__ float residual_term(const I8GemmArgs& p, int row, int col) {
+#pragma clang fp contract(off)
+  const int64_t idx = static_cast<int64_t>(row) * p.residual_sm + col;
+  float r;
+  if (p.residual_dtype == QG_F32) r = static_cast<const float*>(p.residual)[idx];
+  else if (p.residual_dtype == QG_F16) r = f16_to_f32(static_cast<const uint16_t*>(p.residual)[idx]);
+  else r = bf16_to_f32(static_cast<const uint16_t*>(p.residual)[idx]);
+  if (p.residual_scale) r = r * p.residual_scale[p.residual_scalar ? 0 : col];
+  return r;
+}
+
+// Output bits of one element with the residual term (MODE != EPI_INT / EPI_EAGER).
+template <int OUT, int MODE>
+__device__ __forceinline__ uint32_t epi_bits_res(const I8GemmArgs& p, int32_t acc, float sa, float sb, float bv,
+                                                 bool has_bias, int row, int col) {
+#pragma clang fp contract(off)
+  float v = epi_value<OUT, MODE>(acc, sa, sb, bv, has_bias);
+  v = v + residual_term(p, row, col);
+  if constexpr (OUT == QG_F32) return __float_as_uint(v);
+  else if constexpr (OUT == QG_F16) return f32_to_f16(v);
+  else return f32_to_bf16(v);
+}
+
 template <int OUT>
 __device__ __forceinline__ void store_elem(void* out, int64_t idx, uint32_t bits) {
   if constexpr (out_size<OUT>() == 4) static_cast<uint32_t*>(out)[idx] = bits;
@@ -257,7 +281,7 @@ __device__ __forceinline__ EpiParams fetch_epi_params(const I8GemmArgs& p, int m
 // 4 (l >> 5) + (r & 3) and column 32 j + (l & 31) of the wave sub-tile. The
 // caller has drained every copy and passed a barrier after the last LDS read
 // of the rings.
-template <typename G, int OUT, int MODE>
+template <typename G, int OUT, int MODE, bool RES>
 __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&acc)[G::FM][G::FN], char* smem,
                                             int m0, int n0, int wr, int wc, int wave, int lane, int tid,
                                             const EpiParams& ep) {
@@ -310,7 +334,13 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
           static_for<0, G::FN>([&](auto j) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const uint32_t bits = epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias);
+              uint32_t bits;
+              if constexpr (RES)
+                bits = epi_bits_res<OUT, MODE>(p, acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias,
+                                               m0 + wr * G::WM + 32 * i + 8 * q + lh + e,
+                                               n0 + wc * G::WN + j * 32 + lcol);
+              else
+                bits = epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias);
               char* dstp = region + (ii * 32 + 8 * q + lh + e) * ROWB + (j * 32 + lcol) * ES;
               if constexpr (ES == 4) *reinterpret_cast<uint32_t*>(dstp) = bits;
               else *reinterpret_cast<uint16_t*>(dstp) = static_cast<uint16_t>(bits);
@@ -346,7 +376,9 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
               const int row = row0 + 32 * i + 8 * q + e;
               if (row < p.M)
                 store_elem<OUT>(p.out, static_cast<int64_t>(row) * p.N + col,
-                                epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias));
+                                RES ? epi_bits_res<OUT, MODE>(p, acc[i][j][4 * q + e], sa[e], sb[j], bv[j],
+                                                              has_bias, row, col)
+                                    : epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias));
             }
           }
         });
@@ -356,7 +388,7 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
 }
 
 // 4 waves (2 x 2, one per SIMD), the whole next stage staged in registers.
-template <typename G, int WPE, int OUT, int MODE>
+template <typename G, int WPE, int OUT, int MODE, bool RES>
 __global__ __launch_bounds__(G::THREADS, WPE) void k_i8_gemm(I8GemmArgs p) {
 #pragma clang fp contract(off)
   static_assert(G::NW == 4, "register-staged pipeline: 4 waves");
@@ -492,7 +524,7 @@ __global__ __launch_bounds__(G::THREADS, WPE) void k_i8_gemm(I8GemmArgs p) {
   }
 
   wait_vm_barrier<0>();  // no copy into LDS in flight; every wave is done reading the rings
-  i8_epilogue<G, OUT, MODE>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
+  i8_epilogue<G, OUT, MODE, RES>(p, acc, smem, m0, n0, wr, wc, wave, lane, tid, ep);
 }
 
 // 8 waves in two groups that share the SIMDs pairwise (waves w and w + 4) and
@@ -683,7 +715,8 @@ __device__ __forceinline__ f32x4 col4(const float* v, int c0) { return *reinterp
 // column scales and fp32 bias values parked at SC_A, SC_B and SC_BIAS).
 // Full tiles are staged per wave in its own part of the rings and leave as
 // whole 16-byte row chunks; edge tiles store element-wise.
-template <typename G, int OUT, int MODE, int STAGE_BASE = 0, int REGION = G::RING / G::NW, typename ACCV = i32x16>
+template <typename G, int OUT, int MODE, bool RES, int STAGE_BASE = 0, int REGION = G::RING / G::NW,
+          typename ACCV = i32x16>
 __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&acc)[G::FM][G::FN], char* smem,
                                             int m0, int n0, int wr, int wc, int wave, int lane) {
 #pragma clang fp contract(off)
@@ -696,7 +729,9 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
   static_for<0, G::FM>([&](auto i) { sa[i] = MODE != EPI_INT ? sa_lds[wr * G::WM + 32 * i + lr] : 0.0f; });
   // output bits of the 4 columns of quad g of block (i, j): 4 words (4-byte
   // outputs) or 2 packed words (2-byte outputs) in w[0..]
-  auto quad_bits = [&](auto i, auto j, auto g, const f32x4& sb4, const f32x4& bv4, uint32_t (&w)[4]) {
+  // row: the quad's output row; col0: its first output column (residual term)
+  auto quad_bits = [&](auto i, auto j, auto g, const f32x4& sb4, const f32x4& bv4, uint32_t (&w)[4], int row,
+                       int col0) {
     constexpr int r0 = 4 * decltype(g)::value;
     if constexpr (MODE == EPI_INT) {
       static_for<0, 4>([&](auto c) { w[c] = static_cast<uint32_t>(acc[i][j][r0 + decltype(c)::value]); });
@@ -706,6 +741,12 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
         constexpr int C = decltype(c)::value;
         v[C] = epi_value<OUT, MODE>(acc[i][j][r0 + C], sa[i], sb4[C], bv4[C], has_bias);
       });
+      if constexpr (RES) {
+        static_for<0, 4>([&](auto c) {
+          constexpr int C = decltype(c)::value;
+          v[C] = v[C] + residual_term(p, row, min(col0 + C, p.N - 1));
+        });
+      }
       if constexpr (out_size<OUT>() == 4) {
         static_for<0, 4>([&](auto c) { w[c] = __float_as_uint(v[c]); });
       } else {
@@ -743,7 +784,8 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
           static_for<0, PF>([&](auto ii) {
             constexpr int i = decltype(pass)::value * PF + decltype(ii)::value;
             uint32_t w[4];
-            quad_bits(std::integral_constant<int, i>{}, j, g, sb4, bv4, w);
+            quad_bits(std::integral_constant<int, i>{}, j, g, sb4, bv4, w, m0 + wr * G::WM + 32 * i + lr,
+                      n0 + wc * G::WN + c0);
             char* dst = region + (decltype(ii)::value * 32 + lr) * ROWB + c0 * ES;
             if constexpr (ES == 4) *reinterpret_cast<i32x4*>(dst) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
             else *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
@@ -772,7 +814,7 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
         static_for<0, G::FM>([&](auto i) {
           const int row = m0 + wr * G::WM + 32 * decltype(i)::value + lr;
           uint32_t w[4];
-          quad_bits(i, j, g, sb4, bv4, w);
+          quad_bits(i, j, g, sb4, bv4, w, min(row, p.M - 1), n0 + c0);
           if (row < p.M) {
             static_for<0, 4>([&](auto c) {
               constexpr int C = decltype(c)::value;
@@ -797,7 +839,7 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
 // The body is shared by the INT8 kernel (MF = MfmaI8, 1-byte operands) and the
 // 2-byte kernel (MfmaHalf, fp16 / bf16 operands: a 128-byte stage row holds 64
 // K elements, four 32x32x16 k-steps); ES is the operand element size.
-template <typename G, int OUT, int MODE, typename MF, int ES>
+template <typename G, int OUT, int MODE, typename MF, int ES, bool RES>
 __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
 #pragma clang fp contract(off)
   constexpr int YS = pp_copies<G>();
@@ -867,7 +909,7 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
       plan_offsets(m1, n1);
       if (PREF && S > 0) pp_prefetch0<G>(smem, a_base, w_base, voff, wave);
     }
-    pp_epilogue<G, OUT, MODE, EPI_BASE, EPI_REGION>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
+    pp_epilogue<G, OUT, MODE, RES, EPI_BASE, EPI_REGION>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
     if (!more) break;
     wait_lds_barrier();
     t = tn;
@@ -878,9 +920,9 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
   }
 }
 
-template <typename G, int OUT, int MODE>
+template <typename G, int OUT, int MODE, bool RES>
 __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
-  pp_gemm_body<G, OUT, MODE, MfmaI8, 1>(p);
+  pp_gemm_body<G, OUT, MODE, MfmaI8, 1, RES>(p);
 }
 
 // fp16 / bf16 A [M, K] and W [N, K] (K a multiple of 64, 16-byte aligned
@@ -889,7 +931,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
 // decode of W.
 template <typename G, int OUT, bool F16A>
 __global__ __launch_bounds__(G::THREADS, 1) void k_h16_gemm_pp(I8GemmArgs p) {
-  pp_gemm_body<G, OUT, EPI_F, MfmaHalf<F16A>, 2>(p);
+  pp_gemm_body<G, OUT, EPI_F, MfmaHalf<F16A>, 2, false>(p);
 }
 
 __device__ __forceinline__ float silu(float g) {
@@ -1110,21 +1152,30 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
 // CUs of an MI355X (gfx950): the persistent grid size.
 constexpr int kPersistentCUs = 256;
 
-template <typename G, int WPE, int OUT, int MODE>
+template <typename G, int WPE, int OUT, int MODE, bool RES = false>
 hipError_t launch_tile(const I8GemmArgs& p, hipStream_t stream) {
   static_assert(G::LDS_BYTES * WPE <= 160 * 1024, "LDS per CU");
   const int blocks = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
   if constexpr (G::NW == 4)
-    hipLaunchKernelGGL((k_i8_gemm<G, WPE, OUT, MODE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
-  else  // persistent: at most one workgroup per CU (LDS), a multiple of the 8 XCDs
-    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE>), dim3(blocks < kPersistentCUs ? blocks : kPersistentCUs),
+    hipLaunchKernelGGL((k_i8_gemm<G, WPE, OUT, MODE, RES>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
+  else if constexpr (!RES)  // persistent: at most one workgroup per CU (LDS), a multiple of the 8 XCDs
+    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE, false>), dim3(blocks < kPersistentCUs ? blocks : kPersistentCUs),
                        dim3(G::THREADS), 0, stream, p);
+  else
+    return hipErrorInvalidValue;  // launch_i8_gemm sends residual epilogues to the 4-wave kernel
   return hipGetLastError();
 }
 
 template <typename G, int WPE, int OUT>
 hipError_t launch_mode(const I8GemmArgs& p, hipStream_t stream) {
   // Orders F and E coincide for fp32 output (no intermediate rounding).
+  // residual term (qg_w8a8_linear_ex): its own instantiations, so the plain
+  // kernels carry no residual code
+  if (p.residual) {
+    if (p.epi & QG_EPI_GELU_TANH) return launch_tile<G, WPE, OUT, EPI_GELU, true>(p, stream);
+    if (p.epi & QG_EPI_ORDER_FUSED_FMA) return launch_tile<G, WPE, OUT, EPI_FMA, true>(p, stream);
+    return launch_tile<G, WPE, OUT, EPI_F, true>(p, stream);
+  }
   if (p.epi & QG_EPI_GELU_TANH) return launch_tile<G, WPE, OUT, EPI_GELU>(p, stream);
   if (p.epi & QG_EPI_ORDER_FUSED_FMA) return launch_tile<G, WPE, OUT, EPI_FMA>(p, stream);
   if constexpr (OUT != QG_F32) {
@@ -1168,7 +1219,8 @@ hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream) {
   // CUs (4096x3072 -> 256 tiles, x9216 -> 768, x12288 -> 1024). Smaller
   // problems use 128x128 tiles so that more CUs get work.
   const long big = static_cast<long>(ceil_div(p.M, 256)) * ceil_div(p.N, 192);
-  if (big >= 192) return launch_variant<I8Geo<256, 192, 4, 2, 3>, 1>(p, stream);
+  // the residual epilogue (an opt-in path) runs on the 4-wave kernel only
+  if (big >= 192 && p.residual == nullptr) return launch_variant<I8Geo<256, 192, 4, 2, 3>, 1>(p, stream);
   return launch_variant<I8Geo<128, 128, 2, 2, 2>, 2>(p, stream);
 }
 

@@ -22,6 +22,15 @@ struct I8GemmArgs {
   void* out;             // [M, N] contiguous
   int out_dtype;
   int epi;
+  // Optional residual term of the epilogue (nullptr: none): after the scale /
+  // bias / activation steps, v += f32(residual[row * residual_sm + col])
+  // (* residual_scale[col], or residual_scale[0] when residual_scalar), in
+  // fp32 before the one rounding to out_dtype. residual_dtype QG_F32 / F16 / BF16.
+  const void* residual;
+  int residual_dtype;
+  int64_t residual_sm;
+  const float* residual_scale;
+  int residual_scalar;
   // Grouped (MoE) mode (launch_i8_moe_gemm): M is the number of routed rows,
   // tiles [tiles_max][4] = {expert (< 0: none), first row, end of valid rows, -};
   // A row of routed row r is row_token[r] (r when null, < a_rows); expert e's
@@ -72,6 +81,12 @@ hipError_t launch_pack_rows_i8(const int8_t* src, int64_t s_r, int64_t s_k,
                                int64_t k_pad, hipStream_t stream);
 
 // Per-row INT8 quantizer; columns [K, k_pad) of q are written as zeros.
+// Per-row quantizer after a ConvRot rotation of every group of `group` K values
+// (normalised Hadamard, group a power of two in [2, 1024] dividing K,
+// K <= QG_ROT_MAX_K, unit K stride).
+hipError_t launch_rot_quant_rows(const void* x, int x_dtype, int64_t x_sm, int64_t M, int64_t K, int group,
+                                 int8_t* q, int64_t q_sm, int64_t k_pad, float* step, int rounding,
+                                 hipStream_t stream);
 hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t x_sm,
                              int64_t x_sk, int64_t M, int64_t K, int8_t* q,
                              int64_t q_sm, int64_t k_pad, float* step,

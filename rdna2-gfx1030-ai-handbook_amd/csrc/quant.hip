@@ -267,6 +267,81 @@ hipError_t launch_quant_mode(const void* x, int x_dtype, int64_t x_sm, int64_t x
   }
 }
 
+// ConvRot prologue + per-row quantizer: every group of G consecutive K
+// values of the row is rotated by the normalised Hadamard matrix H_G / sqrt(G)
+// (Sylvester order: (H x)_i = sum_j (-1)^popcount(i & j) x_j), then the row is
+// quantized as above. One row per workgroup of 256 threads: the row is held in
+// LDS as fp32 (K <= QG_ROT_MAX_K), transformed in place by the fast
+// Walsh-Hadamard butterflies (log2 G stages of (a, b) -> (a + b, a - b) on
+// pairs h apart inside aligned blocks of 2 h), scaled by the fp32 value of
+// 1 / sqrt(G) (exact for G = 4^j, e.g. 256), then reduced and quantized. The
+// butterflies form the same sums as the dense product with H in another
+// order, so the rotated values agree with it to a few fp32 ulps.
+template <int XT, int MODE>
+__global__ __launch_bounds__(256) void k_rot_quant_rows(const char* x, int64_t x_sm, int K, int G, float inv_sqrt_g,
+                                                        int8_t* q, int64_t q_sm, int k_pad, float* step_out) {
+#pragma clang fp contract(off)
+  constexpr int ES = XType<XT>::size;
+  __shared__ float v[QG_ROT_MAX_K];
+  __shared__ float s_amax[4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int row = blockIdx.x;
+  const char* xr = x + static_cast<int64_t>(row) * x_sm * ES;
+  int8_t* qr = q + static_cast<int64_t>(row) * q_sm;
+  for (int k = t; k < K; k += 256) v[k] = load_x<XT>(xr, k);
+  for (int lh = 0; (1 << lh) < G; ++lh) {
+    const int h = 1 << lh;
+    __syncthreads();
+    for (int b = t; b < K / 2; b += 256) {
+      const int i = ((b >> lh) << (lh + 1)) | (b & (h - 1));
+      const float a = v[i], c = v[i + h];
+      v[i] = a + c;
+      v[i + h] = a - c;
+    }
+  }
+  __syncthreads();
+  float amax = 0.0f;
+  for (int k = t; k < K; k += 256) {
+    const float r = v[k] * inv_sqrt_g;
+    v[k] = r;
+    amax = fmaxf(amax, fabsf(r));
+  }
+  amax = wave_max(amax);
+  if (lane == 0) s_amax[wave] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(s_amax[0], s_amax[1]), fmaxf(s_amax[2], s_amax[3]));
+  const float step = fmaxf(amax / 127.0f, 1.0e-20f);
+  for (int k = t; k < K; k += 256) qr[k] = static_cast<int8_t>(quant_one<MODE>(v[k], step));
+  for (int k = K + t; k < k_pad; k += 256) qr[k] = 0;
+  if (t == 0) step_out[row] = step;
+}
+
+template <int MODE>
+hipError_t launch_rot_quant_mode(const void* x, int x_dtype, int64_t x_sm, int64_t M, int64_t K, int G,
+                                 float inv_sqrt_g, int8_t* q, int64_t q_sm, int64_t k_pad, float* step,
+                                 hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(M));
+  const char* xp = static_cast<const char*>(x);
+  const int k = static_cast<int>(K), kp = static_cast<int>(k_pad);
+  switch (x_dtype) {
+    case QG_F32:
+      hipLaunchKernelGGL((k_rot_quant_rows<QG_F32, MODE>), grid, dim3(256), 0, stream, xp, x_sm, k, G, inv_sqrt_g, q,
+                         q_sm, kp, step);
+      break;
+    case QG_F16:
+      hipLaunchKernelGGL((k_rot_quant_rows<QG_F16, MODE>), grid, dim3(256), 0, stream, xp, x_sm, k, G, inv_sqrt_g, q,
+                         q_sm, kp, step);
+      break;
+    case QG_BF16:
+      hipLaunchKernelGGL((k_rot_quant_rows<QG_BF16, MODE>), grid, dim3(256), 0, stream, xp, x_sm, k, G, inv_sqrt_g,
+                         q, q_sm, kp, step);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void k_pack_rows_i8(const int8_t* src, int64_t s_r, int64_t s_k,
                                                       int64_t rows, int64_t K, int8_t* dst,
                                                       int64_t k_pad) {
@@ -286,6 +361,18 @@ hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t x_sm, int64_t x
   if (rounding == QG_ROUND_HALF_EVEN)
     return launch_quant_mode<QG_ROUND_HALF_EVEN>(x, x_dtype, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
   return launch_quant_mode<QG_ROUND_HALF_AWAY>(x, x_dtype, x_sm, x_sk, M, K, q, q_sm, k_pad, step, stream);
+}
+
+hipError_t launch_rot_quant_rows(const void* x, int x_dtype, int64_t x_sm, int64_t M, int64_t K, int group,
+                                 int8_t* q, int64_t q_sm, int64_t k_pad, float* step, int rounding,
+                                 hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  const float inv_sqrt_g = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(group)));
+  if (rounding == QG_ROUND_HALF_EVEN)
+    return launch_rot_quant_mode<QG_ROUND_HALF_EVEN>(x, x_dtype, x_sm, M, K, group, inv_sqrt_g, q, q_sm, k_pad, step,
+                                                     stream);
+  return launch_rot_quant_mode<QG_ROUND_HALF_AWAY>(x, x_dtype, x_sm, M, K, group, inv_sqrt_g, q, q_sm, k_pad, step,
+                                                   stream);
 }
 
 hipError_t launch_pack_rows_i8(const int8_t* src, int64_t s_r, int64_t s_k, int64_t rows, int64_t K,

@@ -58,6 +58,9 @@ SIGNATURES = {
     "qg_w8a8_linear_workspace_bytes": (_sz, [_p, _i64, _i64, _i64, _i64]),
     "qg_w8a8_linear": (_i, [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _i, _p, _i, _i,
                             _i, _p, _sz, _p]),
+    "qg_rot_quant_rows_i8": (_i, [_p, _i, _i64, _i64, _i64, _i, _p, _i64, _p, _i, _p]),
+    "qg_w8a8_linear_ex": (_i, [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _i, _i, _p, _i, _i64, _p,
+                               _i64, _p, _i, _i, _i, _p, _sz, _p]),
     "qg_w8a8_linear_noalloc": (_i, [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _i, _p, _i, _i,
                                     _i, _p]),
     "qg_w4_pack": (_i, [_p, _i, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _p, _i, _p, _p, _p]),

@@ -37,6 +37,7 @@ import torch
 from . import _kitchen, _lib
 
 _MAX_K = 131071
+_ROT_MAX_K = 16384  # QG_ROT_MAX_K: the ConvRot prologue holds one fp32 row in LDS
 
 
 def _validate(a, b, tile, num_warps, num_stages, group_m):
@@ -174,7 +175,8 @@ def int8_gemm_dequant(a, b, a_scale, b_scale, bias=None, *, tile=(32, 64, 64),
 
 
 def w8a8_linear(x, weight, weight_scale, bias=None, *, out_dtype=None, activation=None,
-                rounding="half_even", epilogue_order="reference"):
+                rounding="half_even", epilogue_order="reference", convrot_groupsize=None, residual=None,
+                residual_scale=None):
     """Fused W8A8 linear: per-token INT8 quantization of ``x`` (absmax/127),
     INT8 MFMA GEMM against ``weight`` [N, K] and the dequant/bias/activation
     epilogue, in one library call (qg_w8a8_linear).
@@ -184,6 +186,21 @@ def w8a8_linear(x, weight, weight_scale, bias=None, *, out_dtype=None, activatio
     rounding: "half_even" (BASELINE per-token rule) or "half_away" (the
     reference's in-tree _quant_rows, fp8_weight_gemm_v06.py:87-90).
     out_dtype defaults to x.dtype.
+
+    Opt-in MOSS steps (qg_w8a8_linear_ex; the MOSS linear applies them around
+    its GEMM at comfy_int8.py:112-122 and :145):
+    convrot_groupsize: a power of two g in [2, 1024] dividing K (MOSS: 256):
+    every group of g values of a row is rotated by H_g / sqrt(g) before the
+    quantizer, with fast Walsh-Hadamard butterflies (the weight must have been
+    rotated the same way when it was quantized). Kitchen's dense fp32 rotation
+    forms the same sums in another order: the rotated values agree to a few
+    fp32 ulps, so a code can differ by one where a quotient sits within a few
+    ulps of a rounding tie.
+    residual: [..., N] fp32/fp16/bf16 (x's leading shape) added in fp32 after
+    the scale, bias and activation steps, times residual_scale (fp32, 1 or N
+    values) when given, before the one rounding to out_dtype: fp32 outputs
+    are Kitchen's fp32 sequence scale -> + bias -> + residual bit for bit.
+    Not with epilogue_order="eager".
     """
     if x.dtype not in _OUT_DTYPES or weight.dtype != torch.int8 or weight.ndim != 2:
         raise TypeError("x must be fp32/fp16/bf16 and weight int8 [N, K]")
@@ -208,12 +225,36 @@ def w8a8_linear(x, weight, weight_scale, bias=None, *, out_dtype=None, activatio
     if bias is not None and (bias.device != x.device or bias.numel() != n or not bias.is_contiguous()
                              or bias.dtype not in _OUT_DTYPES):
         raise ValueError("Bias must be a contiguous floating point vector of length N")
+    if convrot_groupsize is not None:
+        g = int(convrot_groupsize)
+        if g < 2 or g > 1024 or g & (g - 1) or k % g or k > _ROT_MAX_K:
+            raise ValueError(f"ConvRot group size {convrot_groupsize} must be a power of two in [2, 1024] "
+                             f"dividing input features {k} (K <= {_ROT_MAX_K})")
+    if residual is not None:
+        if epilogue_order == "eager":
+            raise ValueError("The residual term is not available with epilogue_order='eager'")
+        if (residual.dtype not in _OUT_DTYPES or residual.device != x.device
+                or tuple(residual.shape) != (*x.shape[:-1], n)):
+            raise ValueError("residual must be a floating point tensor of shape [..., N] on x's device")
+    elif residual_scale is not None:
+        raise ValueError("residual_scale needs a residual")
+    rs = None
+    if residual_scale is not None:
+        rs = residual_scale.reshape(-1)
+        if (rs.dtype != torch.float32 or rs.device != x.device or not rs.is_contiguous()
+                or rs.numel() not in (1, n)):
+            raise ValueError("residual_scale must be contiguous FP32 with 1 or N elements")
     if weight.stride(1) != 1:
         weight = weight.contiguous()
     x2 = x.reshape(-1, k)
     if k and x2.stride(1) != 1:
         x2 = x2.contiguous()
     m = x2.shape[0]
+    r2 = None
+    if residual is not None:
+        r2 = residual.reshape(m, n)
+        if n and r2.stride(1) != 1:
+            r2 = r2.contiguous()
     flags = _epilogue_flags("separate", activation, epilogue_order)
     out = torch.empty((m, n), device=x.device, dtype=out_dtype)
     if m and n:
@@ -221,14 +262,22 @@ def w8a8_linear(x, weight, weight_scale, bias=None, *, out_dtype=None, activatio
         need = lib.qg_w8a8_linear_workspace_bytes(_lib.ptr(weight), weight.stride(0), m, n, k)
         ws = _lib.workspace(need, x.device)
         wsp, wsn = _lib.ws_ptr(ws)
-        status = lib.qg_w8a8_linear(
-            _lib.ptr(x2), _lib.DTYPE_CODE[x2.dtype], x2.stride(0), m, k, _lib.ptr(weight),
-            weight.stride(0), n, _lib.ptr(ws_scale), ws_scale.numel(), _lib.ptr(bias),
-            _lib.DTYPE_CODE[bias.dtype] if bias is not None else 0, _lib.ptr(out),
-            _lib.DTYPE_CODE[out_dtype],
-            _lib.ROUND_HALF_EVEN if rounding == "half_even" else _lib.ROUND_HALF_AWAY,
-            flags, wsp, wsn, _lib.stream_of(x))
-        _lib.check(status, "qg_w8a8_linear")
+        rnd = _lib.ROUND_HALF_EVEN if rounding == "half_even" else _lib.ROUND_HALF_AWAY
+        bias_code = _lib.DTYPE_CODE[bias.dtype] if bias is not None else 0
+        if convrot_groupsize is None and residual is None:
+            status = lib.qg_w8a8_linear(
+                _lib.ptr(x2), _lib.DTYPE_CODE[x2.dtype], x2.stride(0), m, k, _lib.ptr(weight),
+                weight.stride(0), n, _lib.ptr(ws_scale), ws_scale.numel(), _lib.ptr(bias), bias_code,
+                _lib.ptr(out), _lib.DTYPE_CODE[out_dtype], rnd, flags, wsp, wsn, _lib.stream_of(x))
+            _lib.check(status, "qg_w8a8_linear")
+        else:
+            status = lib.qg_w8a8_linear_ex(
+                _lib.ptr(x2), _lib.DTYPE_CODE[x2.dtype], x2.stride(0), m, k, _lib.ptr(weight),
+                weight.stride(0), n, _lib.ptr(ws_scale), ws_scale.numel(), _lib.ptr(bias), bias_code,
+                int(convrot_groupsize or 0), _lib.ptr(r2), _lib.DTYPE_CODE[r2.dtype] if r2 is not None else 0,
+                r2.stride(0) if r2 is not None else 0, _lib.ptr(rs), rs.numel() if rs is not None else 0,
+                _lib.ptr(out), _lib.DTYPE_CODE[out_dtype], rnd, flags, wsp, wsn, _lib.stream_of(x))
+            _lib.check(status, "qg_w8a8_linear_ex")
     return out.reshape(*x.shape[:-1], n)
 
 

@@ -40,3 +40,39 @@ def quantize_int8_rowwise(x, *, rounding="half_even"):
             _lib.stream_of(x))
         _lib.check(status, "qg_quant_rows_i8")
     return q, step
+
+
+def rotate_quantize_int8_rowwise(x, group_size=256, *, rounding="half_even"):
+    """ConvRot then the per-row quantizer in one launch (qg_rot_quant_rows_i8).
+
+    Every group of ``group_size`` (a power of two in [2, 1024] dividing K,
+    K <= 16384) consecutive values of each row of the 2-D [M, K] fp32/fp16/bf16
+    tensor ``x`` is multiplied by H / sqrt(group_size), H the Sylvester
+    Hadamard matrix (Kitchen's _build_hadamard + _rotate_activation at
+    rdna2-ops/rdna2_ops/comfy_int8.py:117-118), then the rows are quantized as
+    by quantize_int8_rowwise. The rotation runs as fast Walsh-Hadamard
+    butterflies in fp32: the same sums as Kitchen's dense product in another
+    order, equal to a few fp32 ulps. Returns (int8 codes [M, K], fp32 steps [M, 1]).
+    """
+    if x.ndim != 2:
+        raise ValueError("Expected a 2-D [M, K] tensor")
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise TypeError("x must be fp32/fp16/bf16")
+    if rounding not in ("half_even", "half_away"):
+        raise ValueError("rounding must be half_even or half_away")
+    m, k = x.shape
+    g = int(group_size)
+    if g < 2 or g > 1024 or g & (g - 1) or k % g or k > 16384:
+        raise ValueError(f"group_size {group_size} must be a power of two in [2, 1024] dividing K={k} "
+                         f"(K <= 16384)")
+    _lib.require_gfx950(x)
+    if k and x.stride(1) != 1:
+        x = x.contiguous()
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    step = torch.empty((m, 1), dtype=torch.float32, device=x.device)
+    if m:
+        status = _lib.library().qg_rot_quant_rows_i8(
+            _lib.ptr(x), _lib.DTYPE_CODE[x.dtype], x.stride(0), m, k, g, _lib.ptr(q), k, _lib.ptr(step),
+            _lib.ROUND_HALF_EVEN if rounding == "half_even" else _lib.ROUND_HALF_AWAY, _lib.stream_of(x))
+        _lib.check(status, "qg_rot_quant_rows_i8")
+    return q, step

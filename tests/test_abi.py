@@ -87,6 +87,43 @@ def test_w8a8_linear_rejects_invalid_arguments(lib):
     assert lib.qg_w8a8_linear_workspace_bytes(p, 64, 4, 4, 64) >= 4 * 64 + 16
 
 
+def test_rot_quant_rows_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(16)
+
+    def call(m=0, k=512, x_dtype=_lib.F32, x_sm=512, g=256, q_sm=512, rounding=0):
+        return lib.qg_rot_quant_rows_i8(p, x_dtype, x_sm, m, k, g, p, q_sm, p, rounding, None)
+
+    assert call() == 0                                     # valid, nothing to do for m = 0
+    for g in (0, 1, 3, 96, 2048):                          # power of two in [2, 1024]
+        assert call(g=g) == INVALID, g
+    assert call(k=384) == INVALID                          # group must divide K (comfy_int8.py:113-116)
+    assert call(k=32768, x_sm=32768, q_sm=32768) == INVALID  # K above QG_ROT_MAX_K
+    assert call(x_dtype=_lib.I8) == INVALID
+    assert call(x_sm=256) == INVALID
+    assert call(q_sm=256) == INVALID
+    assert call(rounding=5) == INVALID
+
+
+def test_w8a8_linear_ex_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(16)
+
+    def call(m=0, k=512, g=0, residual=None, residual_dtype=_lib.F32, residual_sm=64, rs=None, rs_numel=0,
+             epilogue=0):
+        return lib.qg_w8a8_linear_ex(p, _lib.F32, k, m, k, p, k, 64, p, 64, None, 0, g, residual, residual_dtype,
+                                     residual_sm, rs, rs_numel, p, _lib.F32, 0, epilogue, None, 0, None)
+
+    assert call() == 0
+    assert call(g=256, residual=p, rs=p, rs_numel=64) == 0
+    assert call(g=256, residual=p, rs=p, rs_numel=1) == 0
+    assert call(g=384) == INVALID
+    assert call(g=1024, k=1536) == INVALID                 # 1024 does not divide 1536
+    assert call(residual=p, residual_dtype=_lib.I32) == INVALID
+    assert call(residual=p, residual_sm=63) == INVALID      # row stride below N
+    assert call(residual=p, rs=p, rs_numel=7) == INVALID    # residual_scale: 1 or N values
+    assert call(residual=p, epilogue=_lib.EPI_ORDER_EAGER) == INVALID
+    assert call(m=4) == INVALID                            # workspace missing
+
+
 def test_w4a8_gemm_rejects_invalid_arguments(lib):
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     base = dict(a=p, a_sm=256, m=4, k=256, w=p, n=8, group=32, flags=_lib.W4_SIGNED_NIBBLES, scales=p,

@@ -28,7 +28,7 @@ Timing protocol (the reference's, rdna2-ops/bench_int8_gemm.py:259-268):
 the chain (exactly --steps steps per round between synchronisations), the
 cfg0 GEMM and quantizer and the two decode shapes; every figure is the median
 over rounds, the per-round samples are reported. ``clock`` is the GPU's GFX
-clock sampled with amdsmi during those rounds.
+clock read with amdsmi over a 2.5 s window of the same chain after the rounds.
 """
 from __future__ import annotations
 
@@ -37,6 +37,7 @@ import json
 import os
 import statistics
 import sys
+import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -342,8 +343,8 @@ def run_w4a16(torch, lib, _lib, dev, rows=(1, 16, 2048), copies=12):
 def run_fp8(torch, lib, _lib, dev):
     """e4m3 weights with per-channel absmax/448 scales,
     bf16 activations M 4096, K 3072, N 3072 and 12288, bf16 out. Timed per
-    call of qg_fp8w_gemm: on these grids the exact fp8 -> bf16 decode of W into
-    the workspace plus the 2-byte ping-pong GEMM."""
+    call of qg_fp8w_gemm: on these grids the 2-byte ping-pong GEMM with the fp8
+    W stages converted exactly to bf16 in registers."""
     from rdna2_ops import fp8_weight_gemm_v06 as f8
     gen = torch.Generator().manual_seed(3)
     res = {}
@@ -353,7 +354,7 @@ def run_fp8(torch, lib, _lib, dev):
         a = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
         y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
         P = _lib.ptr
-        # workspace: the exactly decoded 2-byte weight on large grids
+        # workspace: packed operands only when they are not canonical
         wsb = lib.qg_fp8w_gemm_workspace_bytes(P(a), k, 1, P(codes), k, 1, m, n, k)
         ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=dev)
 
@@ -471,17 +472,18 @@ def traffic_record(name):
 
 
 class ClockSampler:
-    """Samples the GPU's current GFX (shader) clock with amdsmi from a host
-    thread while the timed rounds run; the samples show the clock the kernels
-    ran at (the MFMA peak assumes 2.4 GHz). Reports nothing if amdsmi cannot
-    read the clock on this box."""
+    """Reads the GPU's GFX (shader) clock with amdsmi from a host thread while
+    the same chain runs back to back for ``seconds``. amdsmi's clock values
+    refresh about once per second, far slower than one timed round, so the
+    clock is read over this separate sustained window rather than during the
+    rounds; samples of the first second (the previous, idle reading) are
+    dropped. Per-XCD clocks come from the GPU metrics table when it has them.
+    Reports nothing if amdsmi cannot read the clock on this box."""
 
-    def __init__(self, period_s=0.002):
+    def __init__(self, period_s=0.05):
         self.period = period_s
         self.samples = []
         self.error = None
-        self._stop = None
-        self._thread = None
         try:
             import amdsmi
             amdsmi.amdsmi_init()
@@ -492,38 +494,55 @@ class ClockSampler:
             self._smi = None
             self.error = f"{type(e).__name__}: {e}"
 
-    def __enter__(self):
-        import threading
+    def _read(self):
+        smi = self._smi
+        try:
+            m = smi.amdsmi_get_gpu_metrics_info(self._handle)
+            xcd = [float(v) for v in (m.get("current_gfxclks") or []) if isinstance(v, (int, float)) and v > 0]
+            if xcd:
+                return sum(xcd) / len(xcd)
+        except Exception:
+            pass
+        info = smi.amdsmi_get_clock_info(self._handle, smi.AmdSmiClkType.GFX)
+        return float(info.get("clk", info.get("cur_clk", 0)))
+
+    def sustained(self, torch, step, seconds=2.5, settle=1.0):
+        """Run ``step()`` back to back for ``seconds`` and sample the clock."""
         if self._smi is None:
             return self
-        self._stop = threading.Event()
+        import threading
+        stop = threading.Event()
+        t0 = time.perf_counter()
 
         def run():
-            while not self._stop.is_set():
+            while not stop.is_set():
                 try:
-                    info = self._smi.amdsmi_get_clock_info(self._handle, self._smi.AmdSmiClkType.GFX)
-                    self.samples.append(float(info.get("clk", info.get("cur_clk", 0))))
+                    v = self._read()
                 except Exception as e:
                     self.error = f"{type(e).__name__}: {e}"
                     return
-                self._stop.wait(self.period)
-        self._thread = threading.Thread(target=run, daemon=True)
-        self._thread.start()
+                if time.perf_counter() - t0 >= settle:
+                    self.samples.append(v)
+                stop.wait(self.period)
+        th = threading.Thread(target=run, daemon=True)
+        th.start()
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(20):
+                step()
+            torch.cuda.synchronize()
+        stop.set()
+        th.join()
         return self
-
-    def __exit__(self, *exc):
-        if self._thread is not None:
-            self._stop.set()
-            self._thread.join()
-        return False
 
     def summary(self):
         if not self.samples:
             return {"source": "amdsmi GFX clock", "available": False, "error": self.error}
         s = sorted(self.samples)
-        return {"source": "amdsmi GFX clock, sampled every 2 ms by a host thread during the timed rounds",
-                "available": True, "median_mhz": s[len(s) // 2], "min_mhz": s[0], "max_mhz": s[-1],
-                "samples": len(s)}
+        return {"source": "amdsmi GFX clock (mean of the XCD clocks), sampled every 50 ms while the chain "
+                          "ran back to back for 2.5 s after the timed rounds (first second dropped: amdsmi "
+                          "refreshes about once per second)",
+                "available": True, "median_mhz": round(s[len(s) // 2], 1), "min_mhz": round(s[0], 1),
+                "max_mhz": round(s[-1], 1), "samples": len(s)}
 
 
 def alternating_rounds(items, rounds):
@@ -599,8 +618,8 @@ def main():
         decode = DecodeW4(torch, lib, _lib, dev)
         items.update(cfg0_gemm=cfg0.time_gemm, cfg0_quant=cfg0.time_quant,
                      w4a16_m1=lambda: decode.time(1), w4a16_m16=lambda: decode.time(16))
-    with ClockSampler() as clock:
-        timed = alternating_rounds(items, args.rounds)
+    timed = alternating_rounds(items, args.rounds)
+    clock = ClockSampler().sustained(torch, chain.step)
     ms, chain_samples = timed["chain"]
     ops = chain.ops()
     value = ops / (ms * 1e-3) / 1e12

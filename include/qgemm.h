@@ -324,11 +324,10 @@ int qg_fp8_decode(const uint8_t* w, int w_dtype, int64_t w_sn, int64_t w_sk,
  * (w_sn, w_sk); out: [m, n] contiguous QG_F16 / QG_BF16 / QG_F32. Operands that
  * are not canonical (unit K stride, 16-byte aligned rows, k % 128 == 0) are
  * packed, zero-padded, into the workspace (qg_fp8w_gemm_workspace_bytes).
- * From 192 output tiles of 256 x 192 on (and 2 * n * k, 2 * m * k < 2^31) the
- * weight is also expanded once per call into the workspace as exact fp16 /
- * bf16 (the activation dtype; every finite fp8 value is exact in both), and
- * the GEMM runs on the 2-byte operands: the same fp32 products and epilogue,
- * another summation order. */
+ * From 192 output tiles of 256 x 192 on (and 2 * m * k < 2^31) the GEMM runs
+ * the 2-byte MFMA on W fragments converted exactly to the activation dtype in
+ * registers (every fp8 value is exact in fp16 and bf16): the same fp32
+ * products and epilogue, another summation order, no extra workspace. */
 size_t qg_fp8w_gemm_workspace_bytes(const void* a, int64_t a_sm, int64_t a_sk,
                                     const uint8_t* w, int64_t w_sn, int64_t w_sk,
                                     int64_t m, int64_t n, int64_t k);

@@ -627,10 +627,10 @@ bool fp8_dtype(int d) { return d == QG_E4M3 || d == QG_E5M2; }
 // multiple of the 128-wide stage; anything else is packed into workspace.
 struct Fp8Plan {
   bool pack_a, pack_w;
-  bool decode;  // large grid: W decoded exactly to A's 2-byte type, then the ping-pong GEMM
+  bool pingpong;  // large grid: the ping-pong GEMM with fp8 W stages converted in registers
   int64_t kp;
-  size_t a_bytes, w_bytes, d_bytes;
-  size_t total() const { return a_bytes + w_bytes + d_bytes; }
+  size_t a_bytes, w_bytes;
+  size_t total() const { return a_bytes + w_bytes; }
 };
 
 Fp8Plan plan_fp8(const void* a, int64_t a_sm, int64_t a_sk, const void* w, int64_t w_sn, int64_t w_sk,
@@ -645,11 +645,10 @@ Fp8Plan plan_fp8(const void* a, int64_t a_sm, int64_t a_sk, const void* w, int64
                 (n - 1) * w_sn + k < kMaxOperandBytes);
   pl.a_bytes = pl.pack_a ? static_cast<size_t>(round_up(2 * m * pl.kp, 256)) : 0;
   pl.w_bytes = pl.pack_w ? static_cast<size_t>(round_up(n * pl.kp, 256)) : 0;
-  // >= 192 tiles of 256 x 192 (the INT8 kernel's large-grid rule) and the
-  // decoded weight addressable with 32-bit offsets: decode + ping-pong GEMM
+  // >= 192 tiles of 256 x 192 (the INT8 kernel's large-grid rule): the
+  // ping-pong GEMM, fp8 W converted exactly to A's 2-byte type in registers
   const int64_t tiles = ((m + 255) / 256) * ((n + 191) / 192);
-  pl.decode = tiles >= 192 && 2 * n * pl.kp < kMaxOperandBytes && 2 * m * pl.kp < kMaxOperandBytes;
-  pl.d_bytes = pl.decode ? static_cast<size_t>(round_up(2 * n * pl.kp, 256)) : 0;
+  pl.pingpong = tiles >= 192 && 2 * m * pl.kp < kMaxOperandBytes;
   return pl;
 }
 
@@ -724,17 +723,14 @@ extern "C" int qg_fp8w_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_
   p.bias_dtype = bias_dtype;
   p.out = out;
   p.out_dtype = out_dtype;
-  if (pl.decode && k > 0) {
-    // every finite fp8 value is exact in fp16 and bf16: decode W once, then the
-    // 2-byte ping-pong GEMM (same fp32 products, order-F epilogue)
-    uint16_t* wd = reinterpret_cast<uint16_t*>(ws + pl.a_bytes + pl.w_bytes);
-    hipError_t e = qg::launch_fp8_expand(p.w8, p.w8_sn, n, pl.kp, p.fp8_e5, wd, p.a_f16 != 0, s);
-    if (e != hipSuccess) return e;
+  if (pl.pingpong && k > 0) {
+    // every fp8 value is exact in fp16 and bf16: the 2-byte ping-pong GEMM with
+    // the W fragments converted in registers (same fp32 products, order F)
     qg::I8GemmArgs g{};
     g.a = reinterpret_cast<const int8_t*>(p.a);
     g.a_sm = p.a_sm;
-    g.w = reinterpret_cast<const int8_t*>(wd);
-    g.w_sn = pl.kp;
+    g.w = reinterpret_cast<const int8_t*>(p.w8);
+    g.w_sn = p.w8_sn;
     g.M = p.M;
     g.N = p.N;
     g.K = p.K;
@@ -746,7 +742,7 @@ extern "C" int qg_fp8w_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_
     g.out = out;
     g.out_dtype = out_dtype;
     g.epi = 0;
-    return qg::launch_h16_gemm(g, p.a_f16 != 0, s);
+    return qg::launch_f8w_gemm(g, p.a_f16 != 0, p.fp8_e5 != 0, s);
   }
   return qg::launch_wd_fp8(p, s);  // k == 0: no stage, out = bias (or 0)
 }

@@ -74,6 +74,13 @@ struct MfmaHalf {
   }
 };
 
+// fp16 / bf16 MFMA whose W fragments arrive as fp8 and are converted in
+// registers (fp8x8, exact).
+template <bool F16, bool E5_>
+struct MfmaHalfF8W : MfmaHalf<F16> {
+  static constexpr bool F16A = F16, E5 = E5_;
+};
+
 enum EpiMode { EPI_INT = 0, EPI_F = 1, EPI_FMA = 2, EPI_EAGER = 3, EPI_GELU = 4 };
 
 // Tile geometry: BM x BN output tile, WGM x WGN waves, A ring of NA slots and
@@ -86,6 +93,7 @@ struct I8Geo {
   static constexpr int FM = WM / 32, FN = WN / 32;    // 32x32 blocks per wave
   static constexpr int KS = 128;                      // K bytes per stage
   static constexpr int KT = KS / 32;                  // MFMA k-steps per stage
+  static constexpr bool W8 = false;                   // W stored as fp8 (1 byte per 2-byte A element)
   static constexpr int STAGE_A = BM * KS, STAGE_B = BN * KS;
   static constexpr int A_SEGS = BM / 8 / NW, B_SEGS = BN / 8 / NW;  // 1 KB copies per wave and stage
   static constexpr int SPW = A_SEGS + B_SEGS;
@@ -99,6 +107,22 @@ struct I8Geo {
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave sub-tile of 32x32 blocks");
   static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0 && NW % 2 == 0, "copies split evenly over waves");
   static_assert(BM <= THREADS && BN <= THREADS, "one epilogue parameter per thread");
+};
+
+// Ping-pong geometry with an fp8 W operand against 2-byte A: a stage holds 64
+// K elements, 128 bytes per A row and 64 bytes per W row, so the W ring is
+// half the size of the 2-byte one.
+template <int BM_, int BN_, int WGM_, int WGN_, int NA_>
+struct F8Geo : I8Geo<BM_, BN_, WGM_, WGN_, NA_> {
+  using Base = I8Geo<BM_, BN_, WGM_, WGN_, NA_>;
+  static constexpr bool W8 = true;
+  static constexpr int KSW = Base::KS / 2;  // W bytes per row and stage
+  static constexpr int STAGE_B = Base::BN * KSW;
+  static constexpr int RING = Base::RING_B + 2 * STAGE_B;
+  static constexpr int SC_A = RING;
+  static constexpr int SC_B = SC_A + Base::BM * 4;
+  static constexpr int SC_BIAS = SC_B + Base::BN * 4;
+  static constexpr int LDS_BYTES = SC_BIAS + Base::BN * 4;
 };
 
 __device__ __forceinline__ float gelu_tanh(float x) {
@@ -571,14 +595,16 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
                                             const char* w_base, const uint32_t (&voff)[pp_copies<G>()], int S,
                                             int wave, int lane, bool pre, Park&& park) {
   static_assert(G::NW == 8 && G::NA == 3 && G::KT == 4, "ping-pong geometry");
-  constexpr int XS = G::BN / 32, YS = G::BM / 32;  // copies per wave and stage (W by X, A by Y)
+  constexpr bool W8 = G::W8;
+  constexpr int KSW = W8 ? G::KS / 2 : G::KS;             // W bytes per row and stage
+  constexpr int XS = G::BN * KSW / 4096, YS = G::BM / 32;  // copies per wave and stage (W by X, A by Y)
   const int wr = wave / G::WGN, wc = wave % G::WGN;
   const bool grp_x = wave < 4;
   const int gw = wave & 3;
   const uint32_t smem_base = lds_addr_of(smem);
   auto copy_w = [&](auto i_c, int s) {
     constexpr int I = decltype(i_c)::value;
-    dma16s(w_base + static_cast<int64_t>(s) * G::KS, voff[I],
+    dma16s(w_base + static_cast<int64_t>(s) * KSW, voff[I],
            smem_base + G::RING_B + (s & 1) * G::STAGE_B + (gw + 4 * I) * 1024);
   };
   auto copy_a = [&](auto i_c, int s) {
@@ -586,11 +612,23 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
     dma16s(a_base + static_cast<int64_t>(s) * G::KS, voff[I], smem_base + (s % 3) * G::STAGE_A + (gw + 4 * I) * 1024);
   };
 
+  // With fp8 W the two k-steps 2u, 2u + 1 of a 32-element K block u take the
+  // K elements {32u + 16h + 0..7} and {32u + 16h + 8..15} from lane half h
+  // (A and W alike, so the dot product is the same sum): one 16-byte read of
+  // W row chunk 2u + h then serves both k-steps. W rows are 64 bytes, their
+  // chunk c stored at c ^ ((row >> 2) & 3) (conflict-free 16-lane reads).
   int a_off[G::KT], b_off[G::KT];
 #pragma unroll
   for (int t = 0; t < G::KT; ++t) {
-    a_off[t] = wr * G::WM * G::KS + frag_offset(t, lane);
-    b_off[t] = G::RING_B + wc * G::WN * G::KS + frag_offset(t, lane);
+    if constexpr (W8) {
+      const int chunk = 4 * (t >> 1) + 2 * (lane >> 5) + (t & 1);
+      a_off[t] = wr * G::WM * G::KS + (lane & 31) * 128 + ((chunk ^ ((lane >> 1) & 7)) << 4);
+      b_off[t] = G::RING_B + wc * G::WN * KSW + (lane & 31) * KSW +
+                 (((2 * (t >> 1) + (lane >> 5)) ^ ((lane >> 2) & 3)) << 4);
+    } else {
+      a_off[t] = wr * G::WM * G::KS + frag_offset(t, lane);
+      b_off[t] = G::RING_B + wc * G::WN * G::KS + frag_offset(t, lane);
+    }
   }
   i32x4 fa[G::KT][G::FM], fb[G::KT][G::FN];
 
@@ -606,9 +644,17 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
       static_for<0, G::FM>([&](auto i) {
         fa[t][i] = *reinterpret_cast<const i32x4*>(smem + abase + a_off[t] + i * 32 * G::KS);
       });
-      static_for<0, G::FN>([&](auto j) {
-        fb[t][j] = *reinterpret_cast<const i32x4*>(smem + bbase + b_off[t] + j * 32 * G::KS);
-      });
+      if constexpr (!W8) {
+        static_for<0, G::FN>([&](auto j) {
+          fb[t][j] = *reinterpret_cast<const i32x4*>(smem + bbase + b_off[t] + j * 32 * G::KS);
+        });
+      } else if constexpr ((t & 1) == 0) {
+        static_for<0, G::FN>([&](auto j) {
+          const i32x4 raw = *reinterpret_cast<const i32x4*>(smem + bbase + b_off[t] + j * 32 * KSW);
+          fb[t][j] = fp8x8<MF::F16A, MF::E5>(static_cast<uint32_t>(raw[0]), static_cast<uint32_t>(raw[1]));
+          fb[t + 1][j] = fp8x8<MF::F16A, MF::E5>(static_cast<uint32_t>(raw[2]), static_cast<uint32_t>(raw[3]));
+        });
+      }
       if constexpr (COPY && X) {
         static_for<t * XS / G::KT, (t + 1) * XS / G::KT>([&](auto d) { copy_w(d, cs); });
       } else if constexpr (COPY) {
@@ -682,7 +728,7 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
 template <typename G>
 __device__ __forceinline__ void pp_prefetch0(char* smem, const char* a_base, const char* w_base,
                                              const uint32_t (&voff)[pp_copies<G>()], int wave) {
-  constexpr int XS = G::BN / 32, YS = G::BM / 32;
+  constexpr int XS = G::BN * (G::W8 ? G::KS / 2 : G::KS) / 4096, YS = G::BM / 32;
   const int gw = wave & 3;
   const uint32_t smem_base = lds_addr_of(smem);
   if (wave < 4) {
@@ -860,9 +906,22 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
 
   // Copy i of a wave covers rows 8 (gw + 4 i) .. + 7 of its operand's tile;
   // the 32-bit row offsets (clamped rows, swizzled chunk) are computed once
-  // per tile.
+  // per tile. fp8 W (64-byte stage rows): copy i covers W rows
+  // 16 (gw + 4 i) .. + 15, lane l fetching chunk (l & 3) ^ ((l >> 4) & 3) of
+  // row l >> 2, which lands at LDS chunk l & 3 of that row (the swizzle the
+  // fragment reads expect).
   uint32_t voff[YS];
   auto plan_offsets = [&](int m0_, int n0_) __attribute__((always_inline)) {
+    if (G::W8 && grp_x) {
+      const int row0 = n0_ + 16 * (wave & 3) + (lane >> 2);
+      const uint32_t chunk16 = static_cast<uint32_t>(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
+      const uint32_t stride = static_cast<uint32_t>(p.w_sn);  // bytes
+      static_for<0, YS>([&](auto i_c) {
+        constexpr int I = decltype(i_c)::value;
+        voff[I] = static_cast<uint32_t>(min(row0 + 64 * I, p.N - 1)) * stride + chunk16;
+      });
+      return;
+    }
     const CopyPlan<4> plan(grp_x ? n0_ : m0_, wave & 3, lane);
     const int rows = grp_x ? p.N : p.M;
     const uint32_t stride = static_cast<uint32_t>((grp_x ? p.w_sn : p.a_sm) * ES);  // bytes
@@ -932,6 +991,15 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
 template <typename G, int OUT, bool F16A>
 __global__ __launch_bounds__(G::THREADS, 1) void k_h16_gemm_pp(I8GemmArgs p) {
   pp_gemm_body<G, OUT, EPI_F, MfmaHalf<F16A>, 2, false>(p);
+}
+
+// fp16 / bf16 A [M, K] against fp8 (e4m3fn or e5m2) W [N, K] (K a multiple of
+// 64, 16-byte aligned rows): W stages stay fp8 in LDS and each fragment is
+// converted exactly to A's type in registers; the products, fp32 accumulation
+// and order-F epilogue are those of k_h16_gemm_pp on the decoded weight.
+template <typename G, int OUT, bool F16A, bool E5>
+__global__ __launch_bounds__(G::THREADS, 1) void k_f8w_gemm_pp(I8GemmArgs p) {
+  pp_gemm_body<G, OUT, EPI_F, MfmaHalfF8W<F16A, E5>, 2, false>(p);
 }
 
 __device__ __forceinline__ float silu(float g) {
@@ -1238,6 +1306,29 @@ hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream) {
   else if (p.out_dtype == QG_BF16) QG_H16(QG_BF16);
   else QG_H16(QG_F32);
 #undef QG_H16
+  return hipGetLastError();
+}
+
+hipError_t launch_f8w_gemm(const I8GemmArgs& p, bool f16a, bool e5, hipStream_t stream) {
+  using G = F8Geo<256, 192, 4, 2, 3>;
+  static_assert(G::LDS_BYTES <= 160 * 1024, "LDS per CU");
+  const int tiles = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
+  if (tiles == 0) return hipSuccess;
+  const dim3 grid(tiles < kPersistentCUs ? tiles : kPersistentCUs);
+#define QG_F8W(OUT, F16, E5)                                                                             \
+  hipLaunchKernelGGL((k_f8w_gemm_pp<G, OUT, F16, E5>), grid, dim3(G::THREADS), 0, stream, p)
+#define QG_F8W_OUT(OUT)                  \
+  do {                                   \
+    if (f16a && e5) QG_F8W(OUT, true, true);        \
+    else if (f16a) QG_F8W(OUT, true, false);        \
+    else if (e5) QG_F8W(OUT, false, true);          \
+    else QG_F8W(OUT, false, false);                 \
+  } while (0)
+  if (p.out_dtype == QG_F16) QG_F8W_OUT(QG_F16);
+  else if (p.out_dtype == QG_BF16) QG_F8W_OUT(QG_BF16);
+  else QG_F8W_OUT(QG_F32);
+#undef QG_F8W_OUT
+#undef QG_F8W
   return hipGetLastError();
 }
 

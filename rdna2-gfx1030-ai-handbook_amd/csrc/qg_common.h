@@ -69,6 +69,40 @@ __device__ __forceinline__ float fp8_to_f32(uint32_t u, bool e5) {
   return __uint_as_float(bits | sign);
 }
 
+// 8 fp8 bytes (2 dwords) -> 8 bf16 / fp16 values in natural order, with
+// gfx950's scaled conversions at scale 1: exact for every e4m3 / e5m2 value
+// (both formats are subsets of fp16 and bf16), NaN and infinity included.
+template <bool F16A, bool E5>
+__device__ __forceinline__ i32x4 fp8x8(uint32_t d0, uint32_t d1) {
+  i32x4 r;
+  if constexpr (F16A) {
+    if constexpr (E5) {
+      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d0, 1.0f, false));
+      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d0, 1.0f, true));
+      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d1, 1.0f, false));
+      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d1, 1.0f, true));
+    } else {
+      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false));
+      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true));
+      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false));
+      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true));
+    }
+  } else {
+    if constexpr (E5) {
+      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d0, 1.0f, false));
+      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d0, 1.0f, true));
+      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d1, 1.0f, false));
+      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d1, 1.0f, true));
+    } else {
+      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, false));
+      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, true));
+      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, false));
+      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, true));
+    }
+  }
+  return r;
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E). Used
 // where every index into a register array must be a constant, independent of
 // the unroller's size heuristics (a dynamic index sends the array to scratch).

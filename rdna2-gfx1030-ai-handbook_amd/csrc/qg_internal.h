@@ -53,6 +53,8 @@ hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream);
 // 2-byte (fp16 / bf16) A and W on the ping-pong main loop; p.a_sm / p.w_sn /
 // p.K in elements, a_scale null (1), b_scale per column or null (1).
 hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream);
+// fp16 / bf16 A against fp8 W converted in registers (fp8 W stages in LDS).
+hipError_t launch_f8w_gemm(const I8GemmArgs& p, bool f16a, bool e5, hipStream_t stream);
 
 // MoE routing and dispatch: see include/qgemm.h (qg_moe_dispatch).
 struct MoeDispatchArgs {
@@ -176,10 +178,6 @@ hipError_t launch_pack_rows_u16(const uint16_t* src, int64_t s_r, int64_t s_k, i
                                 uint16_t* dst, int64_t k_pad, hipStream_t stream);
 hipError_t launch_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64_t n, int64_t K, int e5,
                              void* out, int out_dtype, hipStream_t stream);
-// fp8 -> fp16 / bf16 weight with the hardware conversion (exact for finite
-// values; element-wise decode when rows are not 16-byte aligned).
-hipError_t launch_fp8_expand(const uint8_t* w, int64_t w_sn, int64_t n, int64_t K, int e5, void* out, bool f16,
-                             hipStream_t stream);
 hipError_t launch_wd_fp8(const WdArgs& p, hipStream_t stream);
 
 hipError_t launch_w4a16(const W4Args& p, hipStream_t stream);

@@ -97,38 +97,6 @@ __device__ __forceinline__ void nat_selectors(bool high, uint32_t (&sel)[4]) {
   }
 }
 
-// 8 fp8 bytes (2 dwords) -> 8 bf16 / fp16 values in natural order.
-template <bool F16A, bool E5>
-__device__ __forceinline__ i32x4 fp8x8(uint32_t d0, uint32_t d1) {
-  i32x4 r;
-  if constexpr (F16A) {
-    if constexpr (E5) {
-      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d0, 1.0f, false));
-      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d0, 1.0f, true));
-      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d1, 1.0f, false));
-      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(d1, 1.0f, true));
-    } else {
-      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, false));
-      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d0, 1.0f, true));
-      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, false));
-      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d1, 1.0f, true));
-    }
-  } else {
-    if constexpr (E5) {
-      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d0, 1.0f, false));
-      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d0, 1.0f, true));
-      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d1, 1.0f, false));
-      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d1, 1.0f, true));
-    } else {
-      r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, false));
-      r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, true));
-      r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, false));
-      r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, true));
-    }
-  }
-  return r;
-}
-
 __device__ __forceinline__ float bias_at(const void* bias, int dtype, int col) {
   if (dtype == QG_F32) return static_cast<const float*>(bias)[col];
   const uint16_t b = static_cast<const uint16_t*>(bias)[col];
@@ -460,22 +428,6 @@ __global__ __launch_bounds__(256) void k_fp8_decode16(const uint8_t* w, int64_t 
   }
 }
 
-// fp8 -> 2-byte weight for the decode-then-GEMM path: the hardware conversion
-// of the fused kernel (fp8x8, exact for every finite value), 16 bytes per
-// thread; the element-wise restatement above stays the qg_fp8_decode path.
-template <bool F16A, bool E5>
-__global__ __launch_bounds__(256) void k_fp8_expand16(const uint8_t* w, int64_t w_sn, int n, int K, void* out) {
-  const int cpr = K >> 4;  // 16-byte chunks per row (< 2^27)
-  const int chunks = n * cpr;
-  for (int ci = blockIdx.x * blockDim.x + threadIdx.x; ci < chunks; ci += gridDim.x * blockDim.x) {
-    const int r = ci / cpr, c = ci - r * cpr;
-    const uint4 v = *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(r) * w_sn + 16 * c);
-    i32x4* o = reinterpret_cast<i32x4*>(static_cast<uint16_t*>(out) + static_cast<int64_t>(r) * K + 16 * c);
-    o[0] = fp8x8<F16A, E5>(v.x, v.y);
-    o[1] = fp8x8<F16A, E5>(v.z, v.w);
-  }
-}
-
 unsigned grid_for(int64_t total) {
   const int64_t blocks = ceil_div<int64_t>(total, 256);
   return static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
@@ -510,25 +462,6 @@ hipError_t launch_fp8_decode(const uint8_t* w, int64_t w_sn, int64_t w_sk, int64
   }
   hipLaunchKernelGGL(k_fp8_decode, dim3(grid_for(n * K)), dim3(256), 0, stream, w, w_sn, w_sk, n, K, e5, out,
                      out_dtype);
-  return hipGetLastError();
-}
-
-hipError_t launch_fp8_expand(const uint8_t* w, int64_t w_sn, int64_t n, int64_t K, int e5, void* out, bool f16,
-                             hipStream_t stream) {
-  if (n * K == 0) return hipSuccess;
-  const bool vec = K % 16 == 0 && w_sn % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(out) & 15) == 0 && n * K < (int64_t(1) << 31);
-  if (!vec) return launch_fp8_decode(w, w_sn, 1, n, K, e5, out, f16 ? QG_F16 : QG_BF16, stream);
-  const int64_t chunks = n * K / 16;
-  const dim3 grid(static_cast<unsigned>(chunks / 256 + 1 < 65536 ? chunks / 256 + 1 : 65536));
-  const int ni = static_cast<int>(n), ki = static_cast<int>(K);
-  if (f16) {
-    if (e5) hipLaunchKernelGGL((k_fp8_expand16<true, true>), grid, dim3(256), 0, stream, w, w_sn, ni, ki, out);
-    else hipLaunchKernelGGL((k_fp8_expand16<true, false>), grid, dim3(256), 0, stream, w, w_sn, ni, ki, out);
-  } else {
-    if (e5) hipLaunchKernelGGL((k_fp8_expand16<false, true>), grid, dim3(256), 0, stream, w, w_sn, ni, ki, out);
-    else hipLaunchKernelGGL((k_fp8_expand16<false, false>), grid, dim3(256), 0, stream, w, w_sn, ni, ki, out);
-  }
   return hipGetLastError();
 }
 

@@ -177,16 +177,18 @@ def fp8_weight_gemm(a, w, *, bias=None, method="upcast", prepared=None, tile=(64
         raise ValueError("Unsupported tile or warp count")
     result = _fused(a, w, bias, w_scale)
     if metadata is not None:
-        # the C ABI's choice: >= 192 tiles of 256 x 192 decode W exactly to A's
-        # type and run the 2-byte ping-pong GEMM; smaller grids the fused
-        # decode kernel (256 x 128 tiles from four of them per CU)
+        # the C ABI's choice: >= 192 tiles of 256 x 192 run the 2-byte
+        # ping-pong GEMM with fp8 W stages converted exactly to A's type in
+        # registers; smaller grids the fused decode kernel (256 x 128 tiles
+        # from four of them per CU)
         m, n = a.shape[0], w.shape[0]
         f16 = int(a.dtype == torch.float16)
         kp = -(-a.shape[1] // 128) * 128
-        if (-(-m // 256)) * (-(-n // 192)) >= 192 and 2 * max(m, n) * kp < 2 ** 31:
-            variant = "fp8_decode_f16_pingpong" if f16 else "fp8_decode_bf16_pingpong"
+        if (-(-m // 256)) * (-(-n // 192)) >= 192 and 2 * m * kp < 2 ** 31:
+            variant = "fp8w_f16_pingpong" if f16 else "fp8w_bf16_pingpong"
             tile_used = (256, 192, 64)
-            hint = "k_h16_gemm_ppINS0_5I8GeoILi256ELi192E"
+            hint = "k_f8w_gemm_ppINS0_5F8GeoILi256ELi192ELi4ELi2ELi3EEELi{}ELb{}ELb{}E".format(
+                _lib.DTYPE_CODE[a.dtype], f16, int(w.dtype == torch.float8_e5m2))
         else:
             wide = m >= 256 and (-(-m // 256)) * (-(-n // 128)) >= 4 * 256
             variant, tile_used = "fp8_fused_mfma", ((256, 128, 128) if wide else (128, 128, 128))

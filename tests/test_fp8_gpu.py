@@ -89,9 +89,11 @@ def test_fused_conversion_all_patterns(cuda, e5, adtype):
 @pytest.mark.parametrize("e5", [False, True])
 @pytest.mark.parametrize("adtype", [torch.bfloat16, torch.float16])
 def test_decode_path_conversion_all_patterns(cuda, e5, adtype):
-    """Large grids (>= 192 tiles of 256 x 192) expand the weight into the
-    workspace and run the 2-byte ping-pong GEMM: one-hot activation rows read
-    every finite code of every column back exactly."""
+    """Large grids (>= 192 tiles of 256 x 192) run the 2-byte ping-pong GEMM
+    with fp8 W stages converted in registers (and a K order within each
+    32-element block shared by A and W): one-hot activation rows read every
+    finite code of every column back exactly, so each A element meets the W
+    element of the same K index."""
     case(f"fp8 decode path all patterns e5={e5} {adtype}")
     codes = np.arange(256, dtype=np.uint8)
     vals = o8.decode_bits(codes, e5)
@@ -102,7 +104,7 @@ def test_decode_path_conversion_all_patterns(cuda, e5, adtype):
     a[torch.arange(m), torch.arange(m) % k] = 1
     md = {}
     y = mod().fp8_weight_gemm(a.to(cuda), codes_tensor(wmat, e5, cuda), method="fused_dot2", metadata=md)
-    assert md["launched_tile"] == [256, 192, 64]  # the decode + ping-pong path
+    assert md["launched_tile"] == [256, 192, 64]  # the ping-pong path
     ref = o8.decode_bits(wmat, e5)[:, np.arange(m) % k].T  # out[m, n] = w[n, m % k]
     assert np.array_equal(y.float().cpu().numpy(), ref.astype(np.float32))
 
@@ -254,7 +256,7 @@ def test_cfg3_full_size(cuda, n):
 
 def test_fused_metadata_names_the_launched_tile(cuda):
     """The metadata of the fused method reports the kernel and tile the C ABI
-    chose (decode + 2-byte ping-pong GEMM from 192 tiles of 256 x 192) and
+    chose (the 2-byte ping-pong GEMM on fp8 W from 192 tiles of 256 x 192) and
     that kernel's resources."""
     for m, n, tile in ((128, 256, [128, 128, 128]), (1024, 32768, [256, 192, 64])):
         case(f"fp8 metadata {m}x{n}")

@@ -18,7 +18,9 @@ Prints one JSON line (driver contract). ``value`` = whole-chain TOPS
 around each GEMM launch on its stream inside the timed steps.
 ``roofline_w4a16_decode`` is the metric's second half: the W4A16 decode kernel
 (M = 1) in GB/s against the 8 TB/s HBM peak, timed
-with events around graph replays of 120 launches over 12 rotated weight copies.
+with events around graph replays of 120 launches over 12 rotated weight copies;
+its ``read_floor`` is qg_read_floor over the same byte count, rotated the same
+way (the plain-read floor of this box).
 ``roofline_cfg0`` is the INT8 GEMM alone at BASELINE configuration 0, where
 the metric's >= 60 % bar is quoted. ``secondary`` holds cfg0's quantizer,
 W4A16 M = 16 / 2048, the FP8 configuration 3, MoE (configuration 4) and W4A8.
@@ -236,6 +238,12 @@ class DecodeW4:
             a = torch.randn(m, self.K, generator=gen).to(torch.bfloat16).to(dev)
             y = torch.empty(m, self.N, dtype=torch.bfloat16, device=dev)
             self.graphs[m] = self._capture(m, a, y)
+        # the read floor: qg_read_floor over `copies` buffers of the M = 1
+        # launch's algorithmic bytes, rotated the same way
+        self.floor_bytes = (self.wbytes + self.K * 2 + self.N * 2 + 15) // 16 * 16
+        self.floor_bufs = [torch.ones(self.floor_bytes, dtype=torch.uint8, device=dev) for _ in range(copies)]
+        self.sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.graphs["floor"] = self._capture_floor()
 
     def _call(self, m, a, y, p, stream):
         P, L = self.L.ptr, self.L
@@ -258,6 +266,28 @@ class DecodeW4:
             s.synchronize()
         return g, s, a, y
 
+    def _capture_floor(self):
+        torch, P, L = self.t, self.L.ptr, self.L
+
+        def call(i, stream):
+            L.check(self.lib.qg_read_floor(P(self.floor_bufs[i % self.copies]), self.floor_bytes, P(self.sink),
+                                           stream), "read_floor")
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            for i in range(4):
+                call(i, s.cuda_stream)
+            s.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for i in range(self.launches):
+                    call(i, s.cuda_stream)
+            g.replay()
+            s.synchronize()
+        return g, s, None, None
+
+    def time_floor(self):
+        return self.time("floor")
+
     def time(self, m):
         g, s, _, _ = self.graphs[m]
         torch = self.t
@@ -274,6 +304,12 @@ class DecodeW4:
         gbs = nbytes / (ms * 1e-3) / 1e9
         return {"us": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
                 "TFLOPs": round(2 * m * self.N * self.K / (ms * 1e-3) / 1e12, 1), "bytes": nbytes,
+                "us_by_round": [round(v * 1e3, 2) for v in samples]}
+
+    def floor_result(self, ms, samples):
+        gbs = self.floor_bytes / (ms * 1e-3) / 1e9
+        return {"us": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                "bytes": self.floor_bytes, "kernel": "k_read_floor (qg_read_floor: 2 x 512-thread workgroups per CU, 8 x 1 KB wave requests in flight)",
                 "us_by_round": [round(v * 1e3, 2) for v in samples]}
 
     @staticmethod
@@ -296,6 +332,8 @@ def run_w4a16(torch, lib, _lib, dev, rows=(1, 16, 2048), copies=12):
         for m in dec:
             samples = [d.time(m) for _ in range(3)]
             out[m] = d.result(m, statistics.median(samples), samples)
+        fs = [d.time_floor() for _ in range(3)]
+        out["read_floor"] = d.floor_result(statistics.median(fs), fs)
     if 2048 in rows:
         N, K, G, m = 14336, 4096, 128, 2048
         gen, ps = _w4_weights(torch, dev, 1)
@@ -617,7 +655,8 @@ def main():
         cfg0 = Cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev)
         decode = DecodeW4(torch, lib, _lib, dev)
         items.update(cfg0_gemm=cfg0.time_gemm, cfg0_quant=cfg0.time_quant,
-                     w4a16_m1=lambda: decode.time(1), w4a16_m16=lambda: decode.time(16))
+                     w4a16_m1=lambda: decode.time(1), w4a16_m16=lambda: decode.time(16),
+                     read_floor=decode.time_floor)
     timed = alternating_rounds(items, args.rounds)
     clock = ClockSampler().sustained(torch, chain.step)
     ms, chain_samples = timed["chain"]
@@ -685,6 +724,9 @@ def main():
             "kernel": decode.kernel_name(1) + " (M=1, K 4096, N 14336, g128 uint4, "
                       f"{decode.copies} rotated weight copies)",
             "us_per_launch": dec["us"], "us_by_round": dec["us_by_round"], "algorithmic_bytes": dec["bytes"]}
+        floor = decode.floor_result(*timed["read_floor"])
+        line["roofline_w4a16_decode"]["read_floor"] = floor
+        line["roofline_w4a16_decode"]["frac_of_read_floor"] = round(floor["us"] / dec["us"], 4)
         sec["w4a16_m1"] = w4[1]
         sec["w4a16_m16"] = w4[16]
         pre = run_w4a16(torch, lib, _lib, dev, rows=(2048,))

@@ -76,6 +76,13 @@ extern "C" const char* qg_error_string(int status) {
 
 extern "C" const char* qg_version(void) { return "librdna2_qgemm gfx950 1"; }
 
+extern "C" int qg_read_floor(const void* src, size_t bytes, uint32_t* sink, void* stream) {
+  if (bytes % 16 != 0 || bytes >= (size_t(1) << 40)) return hipErrorInvalidValue;
+  if (bytes == 0) return hipSuccess;
+  if (!src || !sink || !aligned16(src)) return hipErrorInvalidValue;
+  return qg::launch_read_floor(src, bytes, sink, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int qg_quant_rows_i8(const void* x, int x_dtype, int64_t x_sm, int64_t x_sk, int64_t m,
                                 int64_t k, int8_t* q, int64_t q_sm, float* step, int rounding,
                                 void* stream) {

@@ -53,6 +53,8 @@ hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream);
 // 2-byte (fp16 / bf16) A and W on the ping-pong main loop; p.a_sm / p.w_sn /
 // p.K in elements, a_scale null (1), b_scale per column or null (1).
 hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream);
+// Plain streaming read of `bytes` (a multiple of 16) at a 16-byte aligned src.
+hipError_t launch_read_floor(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream);
 // fp16 / bf16 A against fp8 W converted in registers (fp8 W stages in LDS).
 hipError_t launch_f8w_gemm(const I8GemmArgs& p, bool f16a, bool e5, hipStream_t stream);
 

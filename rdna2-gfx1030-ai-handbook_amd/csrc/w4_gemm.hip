@@ -1021,4 +1021,37 @@ hipError_t launch_w4_unpack(const W4Args& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Plain read floor: the bytes are split evenly over the waves of a grid of two
+// 512-thread workgroups per CU; each wave reads its contiguous share as whole
+// 1 KB requests (16 bytes per lane), 8 issued back to back per round, folds
+// them into one word and stores it only if it equals a constant (so the loads
+// stay live).
+__global__ __launch_bounds__(512) void k_read_floor(const char* src, uint64_t bytes, uint64_t share,
+                                                    uint32_t* sink) {
+  constexpr int LPW = 8;
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = static_cast<uint64_t>(blockIdx.x) * 8 + (threadIdx.x >> 6);
+  const uint64_t start = wave * share;
+  const uint64_t end = start + share < bytes ? start + share : bytes;
+  int x = 0;
+  for (uint64_t o = start; o < end; o += LPW * 1024) {
+    i32x4 v[LPW];
+    static_for<0, LPW>([&](auto i) {
+      const uint64_t off = o + 1024u * decltype(i)::value + 16u * lane;
+      v[i] = off < end ? *reinterpret_cast<const i32x4*>(src + off) : i32x4{0, 0, 0, 0};
+    });
+    static_for<0, LPW>([&](auto i) { x ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3]; });
+  }
+  if (x == 0x5eed1e55) sink[0] = static_cast<uint32_t>(x);
+}
+
+hipError_t launch_read_floor(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream) {
+  constexpr uint64_t kWaves = 2 * 256 * 8;  // two workgroups of 8 waves per CU
+  const uint64_t share = ((bytes + kWaves - 1) / kWaves + 1023) / 1024 * 1024;
+  const uint64_t waves = (bytes + share - 1) / share;
+  hipLaunchKernelGGL(k_read_floor, dim3(static_cast<unsigned>((waves + 7) / 8)), dim3(512), 0, stream,
+                     static_cast<const char*>(src), static_cast<uint64_t>(bytes), share, sink);
+  return hipGetLastError();
+}
+
 }  // namespace qg

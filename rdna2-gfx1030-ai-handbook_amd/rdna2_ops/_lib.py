@@ -51,6 +51,7 @@ _p, _i, _i64, _sz, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_
 SIGNATURES = {
     "qg_error_string": (ctypes.c_char_p, [_i]),
     "qg_version": (ctypes.c_char_p, []),
+    "qg_read_floor": (_i, [_p, _sz, _p, _p]),
     "qg_quant_rows_i8": (_i, [_p, _i, _i64, _i64, _i64, _i64, _p, _i64, _p, _i, _p]),
     "qg_int8_gemm_workspace_bytes": (_sz, [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64]),
     "qg_int8_gemm": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i,

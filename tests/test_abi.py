@@ -87,6 +87,15 @@ def test_w8a8_linear_rejects_invalid_arguments(lib):
     assert lib.qg_w8a8_linear_workspace_bytes(p, 64, 4, 4, 64) >= 4 * 64 + 16
 
 
+def test_read_floor_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(16)
+    assert lib.qg_read_floor(p, 0, p, None) == 0                   # nothing to read
+    assert lib.qg_read_floor(p, 24, p, None) == INVALID             # bytes % 16
+    assert lib.qg_read_floor(ctypes.c_void_p(24), 32, p, None) == INVALID  # 16-byte aligned source
+    assert lib.qg_read_floor(None, 32, p, None) == INVALID
+    assert lib.qg_read_floor(p, 32, None, None) == INVALID
+
+
 def test_rot_quant_rows_rejects_invalid_arguments(lib):
     p = ctypes.c_void_p(16)
 

@@ -352,3 +352,17 @@ def test_w4a16_dequant_path_ragged(cuda, adtype, layout, group):
     half = 2.0 ** -11 if adtype == torch.float16 else 2.0 ** -8
     got = y[torch.from_numpy(rows).to(cuda)].float().cpu().numpy().astype(np.float64)
     assert (np.abs(got - yx) <= 1e-2 * rms + half * np.abs(yx) * 1.0001).all(), "BASELINE bar"
+
+
+def test_read_floor_reads_without_writing(cuda):
+    """qg_read_floor (the plain-read floor the decode is measured against)
+    reads a ragged byte count and leaves its sink alone unless the folded word
+    hits its constant."""
+    from rdna2_ops import _lib
+    case("read floor 30.5 MB")
+    buf = torch.ones(30543872 + 48, dtype=torch.uint8, device=cuda)
+    sink = torch.full((1,), 7, dtype=torch.int32, device=cuda)
+    _lib.check(_lib.library().qg_read_floor(_lib.ptr(buf), buf.numel(), _lib.ptr(sink),
+                                            _lib.stream_of(buf)), "qg_read_floor")
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 7

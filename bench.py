@@ -35,6 +35,7 @@ clock read with amdsmi over a 2.5 s window of the same chain after the rounds.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -110,12 +111,14 @@ class Chain:
     def ops(self):
         return sum(2 * self.m * L["n"] * L["k"] for L in self.layers)
 
-    def step(self, events=None):
+    def step(self, events=None, pairs=None):
+        """One chain step. With ``events``, each GEMM launch is bracketed by the
+        next pre-created event pair from the iterator ``pairs`` (no event is
+        created inside a timed region) and (layer, start, end) is appended."""
         for i in range(3):
             self.quant(i)
             if events is not None:
-                e0 = self.t.cuda.Event(enable_timing=True)
-                e1 = self.t.cuda.Event(enable_timing=True)
+                e0, e1 = next(pairs)
                 e0.record(self.stream)
             self.gemm(i)
             if events is not None:
@@ -158,11 +161,15 @@ class Cfg0:
 
     def _time(self, fn):
         e0, e1 = self.t.cuda.Event(enable_timing=True), self.t.cuda.Event(enable_timing=True)
-        e0.record(self.stream)
-        for _ in range(self.iters):
-            fn()
-        e1.record(self.stream)
-        e1.synchronize()
+        gc.disable()
+        try:
+            e0.record(self.stream)
+            for _ in range(self.iters):
+                fn()
+            e1.record(self.stream)
+            e1.synchronize()
+        finally:
+            gc.enable()
         return e0.elapsed_time(e1) / self.iters
 
     def time_gemm(self):
@@ -638,15 +645,25 @@ def main():
     events = []
 
     def chain_round():
-        """Exactly --steps chain steps between two synchronisations; ms per step."""
+        """Exactly --steps chain steps between two synchronisations; ms per step.
+        The per-GEMM timing events are created before the timed region and the
+        garbage collector is paused inside it: creating events there made the
+        host, not the GPU, the bottleneck of one round in several (host enqueue
+        0.77 ms per step against 0.04)."""
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
+        pairs = iter([(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(3 * args.steps)])
         torch.cuda.synchronize()
-        start.record(chain.stream)
-        for _ in range(args.steps):
-            chain.step(events)
-        stop.record(chain.stream)
-        torch.cuda.synchronize()
+        gc.disable()
+        try:
+            start.record(chain.stream)
+            for _ in range(args.steps):
+                chain.step(events, pairs)
+            stop.record(chain.stream)
+            torch.cuda.synchronize()
+        finally:
+            gc.enable()
         return start.elapsed_time(stop) / args.steps
 
     items = {"chain": chain_round}

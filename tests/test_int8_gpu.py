@@ -296,6 +296,44 @@ def test_cfg1_chain_stages(cuda, stage):
         assert not bad.any()
 
 
+def test_cfg1_chain_end_to_end(cuda):
+    """BASELINE config 1 end to end on the GPU (QKV, then MLP up + GELU-tanh,
+    whose fp16 output feeds the down projection), against the oracle chain on
+    96 rows spread over the 4096 tokens (every stage is row-independent).
+    QKV is bit-exact. The down projection's input differs from the oracle's
+    by at most one fp16 ulp (GELU through the hardware exp2 / reciprocal), so
+    the final output is held to the BASELINE bar (1e-2 x RMS plus half an fp16
+    ulp) and to RMS(error) <= 2e-3 x RMS."""
+    from rdna2_ops import synthetic
+    from rdna2_ops.int8_gemm import w8a8_linear
+    from rdna2_ops.quantize import quantize_int8_rowwise
+    case("cfg1 chain end to end")
+    c = synthetic.cfg1()
+    wq_qkv, ws_qkv = quantize_int8_rowwise(c.w_qkv.to(cuda))
+    wq_up, ws_up = quantize_int8_rowwise(c.w_up.to(cuda))
+    wq_dn, ws_dn = quantize_int8_rowwise(c.w_down.to(cuda))
+    x = c.x.to(cuda)
+    qkv = w8a8_linear(x, wq_qkv, ws_qkv, c.b_qkv.to(cuda))
+    h = w8a8_linear(x, wq_up, ws_up, c.b_up.to(cuda), activation="gelu_tanh")
+    y = w8a8_linear(h, wq_dn, ws_dn, c.b_down.to(cuda))
+    assert torch.isfinite(y).all()
+    rows = np.linspace(0, c.x.shape[0] - 1, 96).astype(int)
+    xr = c.x.float().numpy()[rows]
+    ref_qkv, _, _, _ = o.w8a8_linear(xr, wq_qkv.cpu().numpy(), ws_qkv.cpu().numpy().reshape(-1),
+                                     c.b_qkv.float().numpy(), out="f16")
+    assert np.array_equal(f16_bits(qkv[torch.from_numpy(rows).to(cuda)]), o.encode(ref_qkv, "f16").view(np.int16))
+    ref_h, _, _, _ = o.w8a8_linear(xr, wq_up.cpu().numpy(), ws_up.cpu().numpy().reshape(-1),
+                                   c.b_up.float().numpy(), out="f16", activation="gelu_tanh")
+    ref_y, _, _, _ = o.w8a8_linear(o.round_to(ref_h, "f16"), wq_dn.cpu().numpy(), ws_dn.cpu().numpy().reshape(-1),
+                                   c.b_down.float().numpy(), out="f16")
+    got = y[torch.from_numpy(rows).to(cuda)].float().cpu().numpy().astype(np.float64)
+    exp = np.asarray(ref_y, np.float64)
+    err = np.abs(got - exp)
+    rms = float(np.sqrt(np.mean(exp ** 2)))
+    assert (err <= 1e-2 * rms + 2.0 ** -11 * np.abs(exp) * 1.0001).all(), "BASELINE bar"
+    assert float(np.sqrt(np.mean(err ** 2))) <= 2e-3 * rms
+
+
 def test_int8_return_kernel_metadata(cuda):
     """return_kernel names the kernel the C ABI launched (4-wave tile for small
     grids, persistent ping-pong for >= 192 tiles of 256 x 192) with its

@@ -292,7 +292,8 @@ def test_cfg2_prefill_full_size(cuda):
     output is finite; 256 rows spread over M meet the BASELINE bar against the
     exact float64 product, and match the float64 product of the bf16-rounded
     weights the GEMM multiplies within one output rounding plus fp32
-    accumulation slack."""
+    accumulation slack (oracle on the CPU); every output meets the same two
+    bars against those products evaluated in float64 on the GPU."""
     from oracle.int8 import round_to
     case("cfg2 w4a16 m2048 k4096 n14336")
     g = torch.Generator().manual_seed(2)
@@ -316,6 +317,19 @@ def test_cfg2_prefill_full_size(cuda):
     slack = 2.0 ** -17 * (np.abs(av) @ np.abs(wq).T)
     bad = np.abs(got - yq) > 2.0 ** -8 * np.abs(yq) * 1.0001 + slack
     assert not bad.any(), f"{bad.sum()} outputs beyond one rounding of the bf16-weight product"
+    # every output: the same two bars with the products evaluated in float64 on the GPU
+    a64 = a.to(cuda).double()
+    wx = torch.from_numpy((cen.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1))).to(cuda)
+    y_all = a64 @ wx.T
+    err = (y.double() - y_all).abs()
+    rms = y_all.pow(2).mean().sqrt()
+    assert bool((err <= 1e-2 * rms + 2.0 ** -8 * y_all.abs() * 1.0001).all()), "all rows: BASELINE bar"
+    del wx, y_all, err
+    wq64 = torch.from_numpy(wq).to(cuda)
+    yq_all = a64 @ wq64.T
+    slack_all = 2.0 ** -17 * (a64.abs() @ wq64.abs().T)
+    bad_all = (y.double() - yq_all).abs() > 2.0 ** -8 * yq_all.abs() * 1.0001 + slack_all
+    assert int(bad_all.sum()) == 0, "all rows: beyond one rounding of the bf16-weight product"
 
 
 @pytest.mark.parametrize("adtype,layout,group", [(torch.float16, "kn", 64), (torch.bfloat16, "nk", 32)])

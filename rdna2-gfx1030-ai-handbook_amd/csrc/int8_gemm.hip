@@ -590,10 +590,13 @@ constexpr int pp_copies() { return (G::BM > G::BN ? G::BM : G::BN) / 32; }
 // return no copy is in flight and every wave has passed the barrier after the
 // last read of the rings, so each wave may stage its epilogue in its own part
 // of the rings at once (group X's epilogue overlaps group Y's last MFMAs).
-template <typename G, typename MF, typename Park>
+// ST > 0: with `pre` and `stores_fly`, the previous tile's epilogue issued at
+// least ST vector stores per wave after the stage-0 copies; the prologue waits
+// let them stay in flight instead of draining every store first.
+template <typename G, typename MF, int ST = 0, typename Park>
 __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::FN], char* smem, const char* a_base,
                                             const char* w_base, const uint32_t (&voff)[pp_copies<G>()], int S,
-                                            int wave, int lane, bool pre, Park&& park) {
+                                            int wave, int lane, bool pre, Park&& park, bool stores_fly = false) {
   static_assert(G::NW == 8 && G::NA == 3 && G::KT == 4, "ping-pong geometry");
   constexpr bool W8 = G::W8;
   constexpr int KSW = W8 ? G::KS / 2 : G::KS;             // W bytes per row and stage
@@ -686,7 +689,8 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
   if (grp_x) {
     // prologue: W(0) landed everywhere, then read stage 0 and copy W(1)
     if (!pre) static_for<0, XS>([&](auto d) { copy_w(d, 0); });
-    wait_vm<0>();
+    if (ST > 0 && pre && stores_fly) wait_vm<ST>();  // W(0), issued before the stores
+    else wait_vm<0>();
     park();
     wait_lds_barrier();
     if (S > 1) load_phase(T_{}, T_{}, 0, 1);
@@ -700,11 +704,14 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
     }
   } else {
     if (!pre) static_for<0, YS>([&](auto d) { copy_a(d, 0); });
+    const bool fly = ST > 0 && pre && stores_fly;  // A(0) issued before the previous tile's stores
     if (S > 1) {
       static_for<0, YS>([&](auto d) { copy_a(d, 1); });
-      wait_vm<YS>();
+      if (fly) wait_vm<YS + ST>();
+      else wait_vm<YS>();
     } else {
-      wait_vm<0>();
+      if (fly) wait_vm<ST>();
+      else wait_vm<0>();
     }
     park();
     wait_lds_barrier();
@@ -937,6 +944,11 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
   EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
   plan_offsets(m0, n0);
   bool pre = false;
+  bool stores_fly = false;
+  // lower bound of the full-tile epilogue's 16-byte stores per wave (2-byte
+  // outputs; the compiler can only split them into more instructions)
+  constexpr int kStoresPerWave = (PREF && !RES) ? G::FM * (G::WN * out_size<OUT>() / 16) / 2 : 0;
+  static_assert(kStoresPerWave + pp_copies<G>() < 64, "vmcnt range");
   typename MF::acc_t acc[G::FM][G::FN];
   for (;;) {
     // The lane index passes through an opaque copy per tile: lane-derived LDS
@@ -957,7 +969,7 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
         }
       }
     };
-    pp_mainloop<G, MF>(acc, smem, a_base, w_base, voff, S, wave, lane_t, pre, park);
+    pp_mainloop<G, MF, kStoresPerWave>(acc, smem, a_base, w_base, voff, S, wave, lane_t, pre, park, stores_fly);
     const int tn = t + static_cast<int>(gridDim.x);
     const bool more = tn < total;
     int m1 = 0, n1 = 0;
@@ -968,6 +980,12 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
       plan_offsets(m1, n1);
       if (PREF && S > 0) pp_prefetch0<G>(smem, a_base, w_base, voff, wave);
     }
+    // the full-tile epilogue of 2-byte outputs issues kStoresPerWave 16-byte
+    // stores per wave (no other vector memory operation) after the next
+    // tile's stage-0 copies
+    stores_fly = PREF && m0 + G::BM <= p.M && n0 + G::BN <= p.N &&
+                 ((static_cast<int64_t>(p.N) * out_size<OUT>()) % 16) == 0 &&
+                 (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
     pp_epilogue<G, OUT, MODE, RES, EPI_BASE, EPI_REGION>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
     if (!more) break;
     wait_lds_barrier();

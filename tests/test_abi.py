@@ -171,3 +171,18 @@ def test_fp8w_gemm_packs_rows_past_32bit_offsets(lib):
     assert need_a >= 2 * 300 * k                           # A packed
     base = [p, _lib.BF16, k, 1, m, k, p, _lib.E4M3, w_sn, 1, n, None, None, 0, p, _lib.BF16, None, 0, None]
     assert lib.qg_fp8w_gemm(*base) == INVALID              # packing needs workspace
+
+
+
+def test_w4a16_workspace_sizes(lib):
+    """qg_w4a16_gemm_workspace_bytes: the dequantised weight (2 * n * k bytes)
+    for large prefill grids (more than 64 rows, >= 192 tiles of 256 x 192, K a
+    multiple of 64); nothing for decode shapes and small grids, whose kernels
+    read the packed words directly."""
+    zp = _lib.W4_ZEROS_PACKED
+    assert lib.qg_w4a16_gemm_workspace_bytes(2048, 14336, 4096, 128, zp) == 2 * 14336 * 4096
+    assert lib.qg_w4a16_gemm_workspace_bytes(2048, 14336, 4096, 64, 0) == 2 * 14336 * 4096
+    for m in (1, 2, 16, 64):
+        assert lib.qg_w4a16_gemm_workspace_bytes(m, 14336, 4096, 128, zp) == 0
+    assert lib.qg_w4a16_gemm_workspace_bytes(2048, 192, 4096, 128, zp) == 0   # 8 tiles: fused tiled kernel
+    assert lib.qg_w4a16_gemm_workspace_bytes(2048, 14336, 4064, 32, zp) == 0  # K not a multiple of 64

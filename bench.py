@@ -316,7 +316,7 @@ class DecodeW4:
     def floor_result(self, ms, samples):
         gbs = self.floor_bytes / (ms * 1e-3) / 1e9
         return {"us": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
-                "bytes": self.floor_bytes, "kernel": "k_read_floor (qg_read_floor: 2 x 512-thread workgroups per CU, 8 x 1 KB wave requests in flight)",
+                "bytes": self.floor_bytes, "kernel": "k_read_floor (qg_read_floor: 4 x 512-thread workgroups per CU, 4 x 1 KB wave requests in flight)",
                 "us_by_round": [round(v * 1e3, 2) for v in samples]}
 
     @staticmethod

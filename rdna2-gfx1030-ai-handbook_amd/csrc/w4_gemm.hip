@@ -1021,14 +1021,18 @@ hipError_t launch_w4_unpack(const W4Args& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Plain read floor: the bytes are split evenly over the waves of a grid of two
-// 512-thread workgroups per CU; each wave reads its contiguous share as whole
-// 1 KB requests (16 bytes per lane), 8 issued back to back per round, folds
-// them into one word and stores it only if it equals a constant (so the loads
-// stay live).
+// Plain read floor: the bytes are split evenly over the waves of a grid of
+// four 512-thread workgroups per CU; each wave reads its contiguous share as
+// whole 1 KB requests (16 bytes per lane), 4 issued back to back per round,
+// folds them into one word and stores it only if it equals a constant (so the
+// loads stay live). Of the shapes measured for a 30.5 MB read on MI355X (256
+// to 4096 workgroups of 4 to 16 waves, 4 to 16 requests per round, register
+// loads and direct-to-LDS copies), this one and its neighbours are the
+// fastest (6.2-6.3 us); two workgroups per CU with 8 requests per round, the
+// shape of the W4A16 decode, took 6.8 us.
 __global__ __launch_bounds__(512) void k_read_floor(const char* src, uint64_t bytes, uint64_t share,
                                                     uint32_t* sink) {
-  constexpr int LPW = 8;
+  constexpr int LPW = 4;
   const int lane = threadIdx.x & 63;
   const uint64_t wave = static_cast<uint64_t>(blockIdx.x) * 8 + (threadIdx.x >> 6);
   const uint64_t start = wave * share;
@@ -1046,7 +1050,7 @@ __global__ __launch_bounds__(512) void k_read_floor(const char* src, uint64_t by
 }
 
 hipError_t launch_read_floor(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream) {
-  constexpr uint64_t kWaves = 2 * 256 * 8;  // two workgroups of 8 waves per CU
+  constexpr uint64_t kWaves = 4 * 256 * 8;  // four workgroups of 8 waves per CU
   const uint64_t share = ((bytes + kWaves - 1) / kWaves + 1023) / 1024 * 1024;
   const uint64_t waves = (bytes + share - 1) / share;
   hipLaunchKernelGGL(k_read_floor, dim3(static_cast<unsigned>((waves + 7) / 8)), dim3(512), 0, stream,

@@ -277,4 +277,6 @@ def test_fused_metadata_names_the_launched_tile(cuda):
         y = mod().fp8_weight_gemm(a, w, method="fused_dot2", metadata=md)
         assert float(y[0, 0]) == 128 * 2.0 ** -9
         assert md["tile"] == [64, 64, 32]  # the requested tile, as the reference reports it
-        assert md["launched_tile"] == tile and md["vgpr"] is not None and md["spills"] == 0
+        assert md["launched_tile"] == tile and md["vgpr"] is not None
+        # no spill to scratch memory (SGPR spills land in VGPR lanes)
+        assert md["vgpr_spills"] == 0 and md["scratch_bytes"] == 0

@@ -49,6 +49,7 @@ enum WdFormat { WD_W4_UINT4 = 0, WD_W4_GENERIC = 1, WD_FP8_E4M3 = 2, WD_FP8_E5M2
 // 4 x 2 loads every weight column in four waves and is slower still.
 constexpr int kWdWavesM = 2;
 
+
 template <bool F16A>
 __device__ __forceinline__ f32x4 mfma16(const i32x4& a, const i32x4& b, const f32x4& c) {
   if constexpr (F16A)
@@ -364,9 +365,26 @@ hipError_t launch_wd_tile(const WdArgs& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Columns of the W4 tiled kernel's 128-row tile for an M x N output and group G.
+int wd_w4_tile_n(int M, int N, int G) {
+  if (G == 32) return 64;
+  const long tiles = static_cast<long>(ceil_div(M, 128)) * ceil_div(N, 128);
+  return tiles < (G == 64 ? 192 : 256) ? 64 : 128;
+}
+
+// W4 tile width: 128 x 64 tiles where 128 x 128 tiles would leave CUs idle
+// (M = 512, N = 4096: 78.5 -> 52.7 us at group 128, 116 -> 69 us at group 64;
+// M = 1061, N = 3072, 216 tiles: 62.8 -> 58.8 us at group 128, while group 64
+// keeps 128 columns there, 90 against 102 us), and always for group 32, whose
+// 128 x 128 form needs 319 VGPRs (63 spilled: 289 -> 171 us at M = 1061).
 template <int FMT, int G, bool KN>
 hipError_t launch_wd_t(const WdArgs& p, hipStream_t stream) {
-  return launch_wd_tile<FMT, G, KN, 128, 128>(p, stream);
+  if constexpr (G == 32) {
+    return launch_wd_tile<FMT, G, KN, 128, 64>(p, stream);
+  } else {
+    if (wd_w4_tile_n(p.M, p.N, G) == 64) return launch_wd_tile<FMT, G, KN, 128, 64>(p, stream);
+    return launch_wd_tile<FMT, G, KN, 128, 128>(p, stream);
+  }
 }
 
 // dst[r, k] = src[r * s_r + k * s_k] (16-bit) for k < K, 0 for K <= k < k_pad.

@@ -317,7 +317,14 @@ def int4_linear_a16(a, p, *, bias=None, method="dequant", prepared=None, tile=(6
             # 2-byte ping-pong GEMM (256 x 192 tiles, K stage of 64 elements)
             return out, _lib.kernel_metadata("w4a16_dequant_pingpong", (256, 192, 64), "k_h16_gemm_pp")
         if m > 64 and p.k % 128 == 0:
-            return out, _lib.kernel_metadata("w4a16_tiled_mfma", (128, 128, 128), "k_wd_gemm")
+            # 128 x 64 tiles for group 32, and where 128 x 128 tiles would
+            # leave CUs idle (the launcher's wd_w4_tile_n)
+            tiles = -(-m // 128) * -(-p.n // 128)
+            tbn = 64 if p.group_size == 32 or tiles < (192 if p.group_size == 64 else 256) else 128
+            fmt = 0 if (p.flags == _lib.W4_ZEROS_PACKED and p.group_size == 128 and p.scales.dtype != torch.float32) else 1
+            hint = "k_wd_gemmILi{}ELi{}ELb{}ELb{}ELi2ELi4ELi128ELi{}E".format(
+                fmt, p.group_size, int(bool(p.flags & _lib.W4_LAYOUT_KN)), int(a.dtype == torch.float16), tbn)
+            return out, _lib.kernel_metadata("w4a16_tiled_mfma", (128, tbn, 128), hint)
         if m <= 16 and -(-p.k // 128) <= 32:
             if _gemv1_applies(a, p):
                 return out, _lib.kernel_metadata("w4a16_gemv1", (1, 32, 512), "k_w4_gemv1")

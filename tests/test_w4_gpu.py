@@ -266,6 +266,26 @@ def test_w4a16_tiled_all_formats(cuda, g, layout, order, adtype):
         _gemm_case(cuda, m, n, 384, g, sym, layout, order, adtype, bias, seed=m + g)
 
 
+@pytest.mark.parametrize("g,layout,m,n,cols", [(32, "nk", 130, 200, 64), (32, "kn", 1024, 4096, 64),
+                                               (64, "nk", 130, 200, 64), (64, "kn", 1024, 4096, 128),
+                                               (128, "nk", 1024, 4096, 128), (128, "kn", 130, 200, 64)])
+def test_w4a16_tiled_tile_width(cuda, g, layout, m, n, cols):
+    """The tiled kernel's two tile widths: 128 x 64 for group 32 and where 128 x
+    128 tiles would leave CUs idle (fewer than 192 of them for group 64, 256
+    for group 128), else 128 x 128 (1024 x 4096: 256 tiles). Each against the
+    float64 oracle; the metadata names the launched tile and that kernel, which
+    spills nothing to scratch."""
+    case(f"w4a16 tiled width g{g} {layout} m{m} n{n}")
+    _gemm_case(cuda, m, n, 512, g, False, layout, "low", torch.float16, True, seed=m + n + g)
+    rng = np.random.default_rng(g)
+    w = (rng.standard_normal((n, 512)) * 0.02).astype(np.float32)
+    p = w4().pack_int4(torch.from_numpy(w).to(cuda), group_size=g, symmetric=False, layout=layout)
+    a = torch.ones(m, 512, dtype=torch.float16, device=cuda)
+    _, md = w4().int4_linear_a16(a, p, method="dot2", return_kernel=True)
+    assert md["variant"] == "w4a16_tiled_mfma" and md["tile"] == [128, cols, 128], md
+    assert md["vgpr"] is not None and md["vgpr_spills"] == 0 and md["scratch_bytes"] == 0, md
+
+
 def test_w4a16_tiled_uint4_and_f32_out(cuda):
     case("w4a16 tiled uint4 storage, fp32 out")
     rng = np.random.default_rng(12)

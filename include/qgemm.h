@@ -264,8 +264,9 @@ int qg_w4_unpack(const int32_t* data, int64_t n, int64_t k, int group_size,
  * Decode shapes and smaller prefill grids apply each group scale to the exact
  * group partial sum (closer to the exact product than the reference, which
  * rounds every dequantised weight to fp16 first). Prefill grids of more than
- * 64 rows and >= 192 output tiles of 256 x 192 (K a multiple of 64) take the
- * reference's dequant formulation instead: W is dequantised once into the
+ * 64 rows (K a multiple of 64) with at least T output tiles of 256 x 192 —
+ * T = 192 at group 128, 64 at group 64, 1 at group 32 — take the reference's
+ * dequant formulation instead: W is dequantised once into the
  * workspace, (q - z) * s in fp32 rounded to the activation dtype, then a
  * 2-byte MFMA GEMM with fp32 accumulation runs on it; the workspace is then
  * 2 * n * k bytes (16-byte aligned), reported by

@@ -467,15 +467,22 @@ extern "C" int qg_w4_unpack(const int32_t* data, int64_t n, int64_t k, int group
 
 namespace {
 
-// Large prefill grids (more than kW4TiledMinRows rows, >= 192 tiles of
-// 256 x 192 — the INT8 kernel's large-grid rule — and K a multiple of the
-// 64-element stage): W is dequantised once into the workspace as the
-// activation dtype, (q - z) * s in fp32 rounded once (the reference's dequant
-// method, int4_weight_gemm_v07.py:549-554), then the 2-byte ping-pong GEMM
-// runs on it. Returns the workspace bytes (0: the fused tiled kernel).
-size_t w4_prefill_bytes(int64_t m, int64_t n, int64_t k) {
+// Prefill grids (more than kW4TiledMinRows rows, K a multiple of the
+// 64-element stage) with at least as many tiles of 256 x 192 as the dequant
+// formulation needs to beat the fused tiled kernel at that group size: W is
+// dequantised once into the workspace as the activation dtype, (q - z) * s in
+// fp32 rounded once (the reference's dequant method,
+// int4_weight_gemm_v07.py:549-554), then the 2-byte ping-pong GEMM runs on
+// it. Group 128: 192 tiles (the INT8 kernel's large-grid rule); group 64: 64
+// tiles (1061 x 3072 x 3072, 80 tiles: 54-58 us against 74-89 us); group 32:
+// every grid (its four group folds per 128-wide stage make the tiled kernel
+// 2-3x slower: 57-60 against 129-169 us at 1061 x 3072, 71-80 against 86-112
+// us at 512 x 4096, 44 tiles). Returns the workspace bytes (0: the fused
+// tiled kernel).
+size_t w4_prefill_bytes(int64_t m, int64_t n, int64_t k, int group_size) {
   const int64_t tiles = ((m + 255) / 256) * ((n + 191) / 192);
-  if (m <= kW4TiledMinRows || k % 64 != 0 || tiles < 192) return 0;
+  const int64_t min_tiles = group_size == 32 ? 1 : group_size == 64 ? 64 : 192;
+  if (m <= kW4TiledMinRows || k % 64 != 0 || tiles < min_tiles) return 0;
   if (2 * n * k >= kMaxOperandBytes) return 0;
   return static_cast<size_t>(round_up(2 * n * k, 256));
 }
@@ -485,7 +492,7 @@ size_t w4_prefill_bytes(int64_t m, int64_t n, int64_t k) {
 extern "C" size_t qg_w4a16_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int group_size,
                                                 int flags) {
   if (!valid_w4_shape(n, k, group_size, flags) || m < 0 || m > kIntMax) return 0;
-  return w4_prefill_bytes(m, n, k);
+  return w4_prefill_bytes(m, n, k, group_size);
 }
 
 extern "C" int qg_w4a8_gemm(const int8_t* a, int64_t a_sm, int64_t m, int64_t k, const int32_t* w, int64_t n,
@@ -569,9 +576,9 @@ extern "C" int qg_w4a16_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t m
   p.bias_dtype = bias_dtype;
   p.out = out;
   p.out_dtype = out_dtype;
-  // large prefill grids: dequantise W into the workspace, then the 2-byte
-  // ping-pong GEMM (out = acc + bias, one rounding)
-  const size_t need = w4_prefill_bytes(m, n, k);
+  // prefill grids past the group's tile threshold: dequantise W into the
+  // workspace, then the 2-byte ping-pong GEMM (out = acc + bias, one rounding)
+  const size_t need = w4_prefill_bytes(m, n, k, group_size);
   if (need > 0) {
     if (!workspace || workspace_bytes < need || !aligned16(workspace)) return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);

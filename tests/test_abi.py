@@ -176,8 +176,9 @@ def test_fp8w_gemm_packs_rows_past_32bit_offsets(lib):
 
 def test_w4a16_workspace_sizes(lib):
     """qg_w4a16_gemm_workspace_bytes: the dequantised weight (2 * n * k bytes)
-    for large prefill grids (more than 64 rows, >= 192 tiles of 256 x 192, K a
-    multiple of 64); nothing for decode shapes and small grids, whose kernels
+    for prefill grids (more than 64 rows, K a multiple of 64) with at least the
+    group's number of tiles of 256 x 192 (192 at group 128, 64 at group 64, any
+    at group 32); nothing for decode shapes and smaller grids, whose kernels
     read the packed words directly."""
     zp = _lib.W4_ZEROS_PACKED
     assert lib.qg_w4a16_gemm_workspace_bytes(2048, 14336, 4096, 128, zp) == 2 * 14336 * 4096
@@ -186,3 +187,8 @@ def test_w4a16_workspace_sizes(lib):
         assert lib.qg_w4a16_gemm_workspace_bytes(m, 14336, 4096, 128, zp) == 0
     assert lib.qg_w4a16_gemm_workspace_bytes(2048, 192, 4096, 128, zp) == 0   # 8 tiles: fused tiled kernel
     assert lib.qg_w4a16_gemm_workspace_bytes(2048, 14336, 4064, 32, zp) == 0  # K not a multiple of 64
+    assert lib.qg_w4a16_gemm_workspace_bytes(130, 200, 512, 32, 0) == 2 * 200 * 512     # group 32: any grid
+    assert lib.qg_w4a16_gemm_workspace_bytes(130, 200, 512, 64, 0) == 0                 # 2 tiles < 64
+    assert lib.qg_w4a16_gemm_workspace_bytes(1024, 4096, 512, 64, 0) == 2 * 4096 * 512  # 88 tiles >= 64
+    assert lib.qg_w4a16_gemm_workspace_bytes(1024, 4096, 512, 128, zp) == 0             # 88 tiles < 192
+    assert lib.qg_w4a16_gemm_workspace_bytes(64, 200, 512, 32, 0) == 0                  # decode rows

@@ -99,6 +99,7 @@ def test_pack_uint4_baseline(cuda):
 
 
 def _gemm_case(cuda, m, n, k, g, sym, layout, order, adtype, bias, out_dtype=None, a_pad=0, seed=0):
+    from rdna2_ops import _lib
     rng = np.random.default_rng(seed)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     p = w4().pack_int4(torch.from_numpy(w).to(cuda), group_size=g, symmetric=sym, layout=layout, order=order)
@@ -111,7 +112,24 @@ def _gemm_case(cuda, m, n, k, g, sym, layout, order, adtype, bias, out_dtype=Non
     av = act_values(a)
     y64 = o4.w4a16_linear(av, cen, r["scales"], g, act_values(b) if bias else None)
     absmag = o4.w4a16_linear(np.abs(av), np.ones_like(cen), np.abs(r["scales"]), g)
-    check_product(y, y64, absmag, out_dtype or adtype, f"m{m} n{n} k{k} g{g} {layout} {order}")
+    label = f"m{m} n{n} k{k} g{g} {layout} {order}"
+    if _lib.library().qg_w4a16_gemm_workspace_bytes(m, n, k, g, p.flags) > 0:
+        # the dequant formulation: the weights are rounded to the activation
+        # dtype first (the reference's dequant method), so the result is the
+        # rounded-weight product within fp32 accumulation slack and the exact
+        # product within the BASELINE bar
+        wq = w4().unpack_int4(p, dtype=adtype).float().cpu().numpy().astype(np.float64)
+        bias64 = act_values(b) if bias else 0.0
+        yq = av @ wq.T + bias64
+        y32 = w4().w4a16_gemm(a, p, b, out_dtype=torch.float32).cpu().numpy().astype(np.float64)
+        slack = 2.0 ** -17 * (np.abs(av) @ np.abs(wq).T + np.abs(bias64))
+        assert (np.abs(y32 - yq) <= slack).all(), f"{label}: fp32 output vs rounded-weight product"
+        got = y.float().cpu().numpy().astype(np.float64)
+        rms = float(np.sqrt(np.mean(y64 ** 2)))
+        half = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 0.0}[out_dtype or adtype]
+        assert (np.abs(got - y64) <= 1e-2 * rms + half * np.abs(y64) * 1.0001 + 1e-30).all(), f"{label}: BASELINE bar"
+    else:
+        check_product(y, y64, absmag, out_dtype or adtype, label)
 
 
 @pytest.mark.parametrize("g", o4.GROUPS)
@@ -165,7 +183,8 @@ def test_int4_linear_a16_methods(cuda):
     y, md = mod.int4_linear_a16(torch.cat([a] * 8), p, bias=b, method="dot2", return_kernel=True)
     assert md["variant"] == "w4a16_skinny" and md["vgpr"] is not None  # 40 rows
     y, md = mod.int4_linear_a16(torch.cat([a] * 20), p, bias=b, method="dot2", return_kernel=True)
-    assert md["variant"] == "w4a16_tiled_mfma" and md["vgpr"] is not None  # 100 rows
+    # 100 rows at group 32: the dequant formulation (every group-32 prefill grid)
+    assert md["variant"] == "w4a16_dequant_pingpong" and md["vgpr"] is not None
     with pytest.raises(ValueError):
         mod.int4_linear_a16(a.float(), p)
     with pytest.raises(ValueError):
@@ -266,23 +285,28 @@ def test_w4a16_tiled_all_formats(cuda, g, layout, order, adtype):
         _gemm_case(cuda, m, n, 384, g, sym, layout, order, adtype, bias, seed=m + g)
 
 
-@pytest.mark.parametrize("g,layout,m,n,cols", [(32, "nk", 130, 200, 64), (32, "kn", 1024, 4096, 64),
-                                               (64, "nk", 130, 200, 64), (64, "kn", 1024, 4096, 128),
-                                               (128, "nk", 1024, 4096, 128), (128, "kn", 130, 200, 64)])
-def test_w4a16_tiled_tile_width(cuda, g, layout, m, n, cols):
-    """The tiled kernel's two tile widths: 128 x 64 for group 32 and where 128 x
-    128 tiles would leave CUs idle (fewer than 192 of them for group 64, 256
-    for group 128), else 128 x 128 (1024 x 4096: 256 tiles). Each against the
-    float64 oracle; the metadata names the launched tile and that kernel, which
-    spills nothing to scratch."""
-    case(f"w4a16 tiled width g{g} {layout} m{m} n{n}")
+@pytest.mark.parametrize("g,layout,m,n,variant,tile", [
+    (64, "nk", 130, 200, "w4a16_tiled_mfma", [128, 64, 128]),         # 2 tiles of 256 x 192
+    (128, "kn", 130, 200, "w4a16_tiled_mfma", [128, 64, 128]),        # 4 tiles of 128 x 128
+    (128, "nk", 1024, 4096, "w4a16_tiled_mfma", [128, 128, 128]),     # 256 of 128 x 128, 88 of 256 x 192
+    (64, "kn", 1024, 4096, "w4a16_dequant_pingpong", [256, 192, 64]),  # 88 >= 64 tiles of 256 x 192
+    (32, "nk", 130, 200, "w4a16_dequant_pingpong", [256, 192, 64]),    # group 32: every prefill grid
+    (32, "kn", 1024, 4096, "w4a16_dequant_pingpong", [256, 192, 64])])
+def test_w4a16_prefill_kernel_choice(cuda, g, layout, m, n, variant, tile):
+    """Prefill grids (M > 64, K 512): the tiled kernel's two tile widths (128 x 64
+    where 128 x 128 tiles would leave CUs idle, else 128 x 128), and the dequant
+    formulation from the group's tile threshold (192 tiles of 256 x 192 at group
+    128, 64 at group 64, every grid at group 32). Each against the float64
+    oracle (the dequant formulation against the rounded-weight product); the
+    metadata names the launched kernel and tile, which spill nothing to scratch."""
+    case(f"w4a16 prefill choice g{g} {layout} m{m} n{n}")
     _gemm_case(cuda, m, n, 512, g, False, layout, "low", torch.float16, True, seed=m + n + g)
     rng = np.random.default_rng(g)
     w = (rng.standard_normal((n, 512)) * 0.02).astype(np.float32)
     p = w4().pack_int4(torch.from_numpy(w).to(cuda), group_size=g, symmetric=False, layout=layout)
     a = torch.ones(m, 512, dtype=torch.float16, device=cuda)
     _, md = w4().int4_linear_a16(a, p, method="dot2", return_kernel=True)
-    assert md["variant"] == "w4a16_tiled_mfma" and md["tile"] == [128, cols, 128], md
+    assert md["variant"] == variant and md["tile"] == tile, md
     assert md["vgpr"] is not None and md["vgpr_spills"] == 0 and md["scratch_bytes"] == 0, md
 
 

@@ -309,12 +309,16 @@ def int4_linear_a16(a, p, *, bias=None, method="dequant", prepared=None, tile=(6
         bias = bias.contiguous()
     out = w4a16_gemm(a, p, bias)
     if return_kernel:
-        # the C ABI's choice: the tiled MFMA kernel past 64 rows (K a multiple of
-        # 128), the decode kernel for up to 16 rows and K <= 4096, else skinny
+        # the C ABI's choice: past 64 rows the dequant formulation from the
+        # group's tile threshold (K a multiple of 64), else the tiled MFMA kernel
+        # (K a multiple of 128); the decode kernels for up to 16 rows and K <=
+        # 4096; else skinny
         m = a.shape[0]
         if _lib.library().qg_w4a16_gemm_workspace_bytes(m, p.n, p.k, p.group_size, p.flags) > 0:
-            # large prefill grid: W dequantised into the workspace, then the
-            # 2-byte ping-pong GEMM (256 x 192 tiles, K stage of 64 elements)
+            # prefill grid at or past the group's threshold of 256 x 192 tiles
+            # (192 at group 128, 64 at group 64, any at group 32): W
+            # dequantised into the workspace, then the 2-byte ping-pong GEMM
+            # (256 x 192 tiles, K stage of 64 elements)
             return out, _lib.kernel_metadata("w4a16_dequant_pingpong", (256, 192, 64), "k_h16_gemm_pp")
         if m > 64 and p.k % 128 == 0:
             # 128 x 64 tiles for group 32, and where 128 x 128 tiles would

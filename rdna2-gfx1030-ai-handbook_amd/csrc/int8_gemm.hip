@@ -160,6 +160,9 @@ __device__ __forceinline__ float round_to(float v) {
 template <int OUT>
 constexpr int out_size() { return (OUT == QG_F16 || OUT == QG_BF16) ? 2 : 4; }
 
+// Row stride (elements) of a dense kernel's output: out_sm, or N when 0.
+__device__ __forceinline__ int64_t out_ld(const I8GemmArgs& p) { return p.out_sm > 0 ? p.out_sm : p.N; }
+
 // Storage bits of one output element.
 //   EPI_F:     v = f32(acc) * (sa * sb); v = v + bias           (int8_gemm.py:53-63)
 //   EPI_FMA:   v = fma(f32(acc), sa * sb, bias)                 (rounding="fused", :191)
@@ -337,7 +340,8 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
   };
 
   constexpr int ES = out_size<OUT>();
-  const bool full = m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((static_cast<int64_t>(p.N) * ES) % 16) == 0 &&
+  const int64_t ldo = out_ld(p);
+  const bool full = m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((ldo * ES) % 16) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
   if (full) {
     // Stage the rounded wave sub-tile in LDS (PF blocks of 32 rows per pass, own
@@ -382,7 +386,7 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
         const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
         const int64_t grow = m0 + wr * G::WM + decltype(pass)::value * PF * 32 + rr;
         const int64_t gcol = n0 + wc * G::WN;
-        *reinterpret_cast<i32x4*>(out + (grow * p.N + gcol) * ES + cc * 16) = v;
+        *reinterpret_cast<i32x4*>(out + (grow * ldo + gcol) * ES + cc * 16) = v;
       }
     });
   } else {
@@ -399,7 +403,7 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
             for (int e = 0; e < 4; ++e) {
               const int row = row0 + 32 * i + 8 * q + e;
               if (row < p.M)
-                store_elem<OUT>(p.out, static_cast<int64_t>(row) * p.N + col,
+                store_elem<OUT>(p.out, static_cast<int64_t>(row) * ldo + col,
                                 RES ? epi_bits_res<OUT, MODE>(p, acc[i][j][4 * q + e], sa[e], sb[j], bv[j],
                                                               has_bias, row, col)
                                     : epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias));
@@ -818,7 +822,8 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
   };
 
   constexpr int ES = out_size<OUT>();
-  const bool full = m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((static_cast<int64_t>(p.N) * ES) % 16) == 0 &&
+  const int64_t ldo = out_ld(p);
+  const bool full = m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((ldo * ES) % 16) == 0 &&
                     (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
   if (full) {
     // PF blocks of 32 rows per pass through the wave's staging region
@@ -855,7 +860,7 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
         const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
         const int64_t grow = m0 + wr * G::WM + decltype(pass)::value * PF * 32 + rr;
         const int64_t gcol = n0 + wc * G::WN;
-        *reinterpret_cast<i32x4*>(out + (grow * p.N + gcol) * ES + cc * 16) = v;
+        *reinterpret_cast<i32x4*>(out + (grow * ldo + gcol) * ES + cc * 16) = v;
       }
     });
   } else {
@@ -873,7 +878,7 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
               constexpr int C = decltype(c)::value;
               const int col = n0 + c0 + C;
               const uint32_t bits = ES == 4 ? w[C] : (w[C / 2] >> (16 * (C & 1))) & 0xffffu;
-              if (col < p.N) store_elem<OUT>(p.out, static_cast<int64_t>(row) * p.N + col, bits);
+              if (col < p.N) store_elem<OUT>(p.out, static_cast<int64_t>(row) * ldo + col, bits);
             });
           }
         });
@@ -896,7 +901,9 @@ template <typename G, int OUT, int MODE, typename MF, int ES, bool RES>
 __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
 #pragma clang fp contract(off)
   constexpr int YS = pp_copies<G>();
-  constexpr bool PREF = out_size<OUT>() == 2;
+  // the next tile's stage-0 prefetch needs 32 staged output rows of a wave to
+  // fit in A slots 1-2 (2-byte outputs of the 256-row tiles)
+  constexpr bool PREF = out_size<OUT>() == 2 && 32 * (G::WN * 2 + 16) <= (G::NA - 1) * G::STAGE_A / G::NW;
   constexpr int EPI_BASE = PREF ? G::STAGE_A : 0;
   constexpr int EPI_REGION = PREF ? (G::NA - 1) * G::STAGE_A / G::NW : G::RING / G::NW;
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
@@ -983,8 +990,7 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     // the full-tile epilogue of 2-byte outputs issues kStoresPerWave 16-byte
     // stores per wave (no other vector memory operation) after the next
     // tile's stage-0 copies
-    stores_fly = PREF && m0 + G::BM <= p.M && n0 + G::BN <= p.N &&
-                 ((static_cast<int64_t>(p.N) * out_size<OUT>()) % 16) == 0 &&
+    stores_fly = PREF && m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((out_ld(p) * out_size<OUT>()) % 16) == 0 &&
                  (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
     pp_epilogue<G, OUT, MODE, RES, EPI_BASE, EPI_REGION>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
     if (!more) break;
@@ -1310,8 +1316,46 @@ hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream) {
   return launch_variant<I8Geo<128, 128, 2, 2, 2>, 2>(p, stream);
 }
 
-hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream) {
-  using G = I8Geo<256, 192, 4, 2, 3>;
+namespace {
+
+// Tail split of a persistent launch of BM x BN tiles. When the tiles take more
+// than one round of kPersistentCUs workgroups and the last round would run
+// one big tile per busy CU while the rest wait, columns [0, n1) keep the big
+// tiles in whole rounds and columns [n1, N) run as a single round of 128 x 128
+// tiles (a third of a 256 x 192 tile's work each), so the last round takes
+// about half the time. Returns n1, or 0 for no split (whole rounds already,
+// a single round, or a remainder that needs more than one round of small
+// tiles).
+template <int BM, int BN>
+int tail_split_cols(int M, int N) {
+  const long nbm = ceil_div(M, BM), nbn = ceil_div(N, BN);
+  const long tiles = nbm * nbn;
+  if (tiles <= kPersistentCUs || tiles % kPersistentCUs == 0) return 0;
+  const long c1 = tiles / kPersistentCUs * kPersistentCUs / nbm;  // column tiles in whole rounds
+  if (c1 <= 0 || c1 >= nbn) return 0;
+  const int n1 = static_cast<int>(c1) * BN;
+  const long rem = static_cast<long>(ceil_div(M, 128)) * ceil_div(N - n1, 128);
+  return rem <= kPersistentCUs ? n1 : 0;
+}
+
+// Columns [n1, N) of p as a problem of its own: W rows, column scales, bias
+// values and output columns start at n1, and the output keeps p's row stride.
+// w_es: bytes per W element.
+I8GemmArgs column_slice(const I8GemmArgs& p, int n1, int w_es) {
+  I8GemmArgs q = p;
+  q.N = p.N - n1;
+  q.w = p.w + static_cast<int64_t>(n1) * p.w_sn * w_es;
+  if (p.b_scale != nullptr && !p.b_scalar) q.b_scale = p.b_scale + n1;
+  if (p.bias != nullptr) q.bias = static_cast<const char*>(p.bias) + static_cast<int64_t>(n1) * (p.bias_dtype == QG_F32 ? 4 : 2);
+  const int out_es = (p.out_dtype == QG_F16 || p.out_dtype == QG_BF16) ? 2 : 4;
+  q.out = static_cast<char*>(p.out) + static_cast<int64_t>(n1) * out_es;
+  q.out_sm = p.out_sm > 0 ? p.out_sm : p.N;
+  return q;
+}
+
+template <typename G>
+hipError_t launch_h16_geo(const I8GemmArgs& p, bool f16a, hipStream_t stream) {
+  static_assert(G::LDS_BYTES <= 160 * 1024, "LDS per CU");
   const int tiles = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
   if (tiles == 0) return hipSuccess;
   const dim3 grid(tiles < kPersistentCUs ? tiles : kPersistentCUs);
@@ -1325,6 +1369,20 @@ hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream) {
   else QG_H16(QG_F32);
 #undef QG_H16
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream) {
+  using Big = I8Geo<256, 192, 4, 2, 3>;
+  const int n1 = tail_split_cols<Big::BM, Big::BN>(p.M, p.N);
+  if (n1 == 0) return launch_h16_geo<Big>(p, f16a, stream);
+  I8GemmArgs head = p;
+  head.N = n1;
+  head.out_sm = p.out_sm > 0 ? p.out_sm : p.N;
+  const hipError_t e = launch_h16_geo<Big>(head, f16a, stream);
+  if (e != hipSuccess) return e;
+  return launch_h16_geo<I8Geo<128, 128, 4, 2, 3>>(column_slice(p, n1, 2), f16a, stream);
 }
 
 hipError_t launch_f8w_gemm(const I8GemmArgs& p, bool f16a, bool e5, hipStream_t stream) {

@@ -19,7 +19,7 @@ struct I8GemmArgs {
   int b_scalar;
   const void* bias;      // nullptr or [N] of bias_dtype
   int bias_dtype;
-  void* out;             // [M, N] contiguous
+  void* out;             // [M, N], row stride out_sm (0: N)
   int out_dtype;
   int epi;
   // Optional residual term of the epilogue (nullptr: none): after the scale /
@@ -42,7 +42,7 @@ struct I8GemmArgs {
   int64_t w_estride;
   const float* row_weight;
   const int* row_slot;
-  int64_t out_sm;
+  int64_t out_sm;  // row stride of out in elements (the dense kernels read 0 as N)
   int out_rows;   // rows of out (routed rows, or tokens * top_k for the route epilogue)
   int n_experts;
   int moe_epi;

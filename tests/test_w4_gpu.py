@@ -376,16 +376,22 @@ def test_cfg2_prefill_full_size(cuda):
     assert int(bad_all.sum()) == 0, "all rows: beyond one rounding of the bf16-weight product"
 
 
-@pytest.mark.parametrize("adtype,layout,group", [(torch.float16, "kn", 64), (torch.bfloat16, "nk", 32)])
-def test_w4a16_dequant_path_ragged(cuda, adtype, layout, group):
-    """The dequant path on a ragged grid (M 1100, N 7500: 200 tiles of
-    256 x 192, partial edge tiles) with the reference's signed storage, bias and
-    fp32 output: the weights are dequantised to the activation dtype, so the
-    result matches the float64 product of those rounded weights within fp32
-    accumulation slack, and the exact product within the BASELINE bar."""
+@pytest.mark.parametrize("adtype,layout,group,m,n", [
+    (torch.float16, "kn", 64, 1100, 7500), (torch.bfloat16, "nk", 32, 1100, 7500),
+    (torch.bfloat16, "nk", 128, 2000, 6344), (torch.float16, "kn", 32, 2000, 6344)])
+def test_w4a16_dequant_path_ragged(cuda, adtype, layout, group, m, n):
+    """The dequant path on ragged grids with the reference's signed storage,
+    bias and fp32 output. M 1100, N 7500: 200 tiles of 256 x 192 with partial
+    edge tiles, one launch. M 2000, N 6344: 272 tiles, so the GEMM splits into
+    columns [0, 6144) in one whole round of 256 x 192 tiles and a tail of
+    128 x 128 tiles over columns [6144, 6344) (a partial column tile, ragged
+    rows) that writes at the output's full row stride. The weights are
+    dequantised to the activation dtype, so the result matches the float64
+    product of those rounded weights within fp32 accumulation slack, and the
+    exact product within the BASELINE bar; the sampled rows cover both parts."""
     from oracle.int8 import round_to
-    case(f"w4a16 dequant path m1100 n7500 k512 {adtype} {layout} g{group}")
-    m, n, k = 1100, 7500, 512
+    case(f"w4a16 dequant path m{m} n{n} k512 {adtype} {layout} g{group}")
+    k = 512
     rng = np.random.default_rng(group)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     p = w4().pack_int4(torch.from_numpy(w).to(cuda), group_size=group, symmetric=False, layout=layout)

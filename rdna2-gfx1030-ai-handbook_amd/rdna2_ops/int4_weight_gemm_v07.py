@@ -318,7 +318,9 @@ def int4_linear_a16(a, p, *, bias=None, method="dequant", prepared=None, tile=(6
             # prefill grid at or past the group's threshold of 256 x 192 tiles
             # (192 at group 128, 64 at group 64, any at group 32): W
             # dequantised into the workspace, then the 2-byte ping-pong GEMM
-            # (256 x 192 tiles, K stage of 64 elements)
+            # (256 x 192 tiles, K stage of 64 elements; a grid past one round
+            # of the 256 CUs whose last round would be partly idle runs its
+            # remaining columns as one more launch of 128 x 128 tiles)
             return out, _lib.kernel_metadata("w4a16_dequant_pingpong", (256, 192, 64), "k_h16_gemm_pp")
         if m > 64 and p.k % 128 == 0:
             # 128 x 64 tiles for group 32, and where 128 x 128 tiles would

@@ -1026,18 +1026,27 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_f8w_gemm_pp(I8GemmArgs p) {
   pp_gemm_body<G, OUT, EPI_F, MfmaHalfF8W<F16A, E5>, 2, false>(p);
 }
 
+// Raw buffer resources (stride 0, range checked against num_records bytes):
+// the gfx9 descriptor word 3 (32-bit data format), and an offset that no
+// buffer this library builds reaches (their num_records stay at or below
+// it), so a store at it is dropped by the range check.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr uint32_t kOobOffset = 0x7FFFFFF0u;
+
 __device__ __forceinline__ float silu(float g) {
 #pragma clang fp contract(off)
   // g / (1 + e^-g) with the hardware exp2 and reciprocal (a few ulps)
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
 }
 
-// Grouped (MoE) INT8 GEMM on the ping-pong main loop. The grid walks the
-// device tile table (tiles_max tiles of G::BM routed rows x ceil(N / G::BN)
-// column tiles): tile t = {expert e (< 0: none), first routed row m0, end of
-// the expert's valid rows}; tile 0's spare field holds the number of tiles in
-// use. A row of routed row r is row_token[r] (or r), W and b_scale start at
-// expert e. Epilogues (v = f32(acc) * (sa[r] * sb[e, n]), order F):
+// Grouped (MoE) INT8 GEMM on the ping-pong main loop, persistent. Work items
+// are the device tile table's tiles in use (tile 0's spare field holds their
+// number) x ceil(N / G::BN) column tiles: tile t = {expert e (< 0: none), first
+// routed row m0, end of the expert's valid rows}. Each XCD takes one
+// contiguous range of items and workgroup b (XCD b & 7) every (gridDim.x /
+// 8)-th item of its range, skipping table entries that name no tile. A row of
+// routed row r is row_token[r] (or r); W and b_scale start at expert e.
+// Epilogues (v = f32(acc) * (sa[r] * sb[e, n]), order F):
 //   QG_MOE_EPI_I32       out int32 [M, N] = acc (routed rows)
 //   QG_MOE_EPI_SILU_MUL  columns 32 b .. 32 b + 15 are the gate and
 //                        32 b + 16 .. 32 b + 31 the up rows of features
@@ -1045,10 +1054,21 @@ __device__ __forceinline__ float silu(float g) {
 //                        (in the transposed layout the gate and up values of
 //                        a feature sit in the same lane, registers r and r + 8)
 //   QG_MOE_EPI_ROUTE     out bf16 [slots, N] row row_slot[r] = v * row_weight[r]
+// As in the dense persistent body, the next item's table entry, copy offsets
+// and per-row parameters are read and its stage-0 copies (A slot 0, W slot 0)
+// issued before the current item's epilogue, which stages its bf16 rows 32 at
+// a time in A slots 1-2; a barrier after the epilogue keeps the next item's
+// parked parameters and stage-1 copies off the LDS the epilogue still reads.
+// The staged epilogue's stores are buffer stores whose lanes without a
+// valid target get an offset past the buffer's range, which the hardware
+// drops: every wave issues the same number of them per item, so the next
+// main loop lets them fly past its stage-0 waits (as the dense body does).
 template <typename G, int MOE>
 __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
 #pragma clang fp contract(off)
   constexpr int YS = pp_copies<G>();
+  constexpr int EPI_BASE = G::STAGE_A;                              // A slots 1-2
+  constexpr int EPI_REGION = (G::NA - 1) * G::STAGE_A / G::NW;     // bytes per wave
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES + 8 * G::BM];
 
   const int tid = threadIdx.x;
@@ -1057,187 +1077,233 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
   const int wr = wave / G::WGN, wc = wave % G::WGN;
   const bool grp_x = wave < 4;
 
-  // Tiles in use (from the dispatch) x column tiles, spread as contiguous
-  // ranges over the 8 XCDs; the rest of the grid exits at once.
   const int ncol = ceil_div(p.N, G::BN);
   const int used = min(max(p.tiles[3], 0), p.tiles_max) * ncol;
-  const int bid0 = blockIdx.x;
-  if (bid0 >= ((used + 7) & ~7)) return;
   const int per_xcd = (used + 7) >> 3;
-  const int bid = (bid0 & 7) * per_xcd + (bid0 >> 3);
-  if (bid >= used) return;
-  const int tile = bid / ncol, ct = bid - tile * ncol;
-  const int e = p.tiles[4 * tile];
-  const int m0 = p.tiles[4 * tile + 1], m_end = p.tiles[4 * tile + 2];
-  // whole workgroup: no tile, or a table entry outside the operands
-  if (e < 0 || e >= p.n_experts || m0 < 0 || m0 >= p.M || m_end <= m0 || m_end > p.M) return;
-  const int n0 = ct * G::BN;
+  const int slots = static_cast<int>(gridDim.x) >> 3;  // the grid is a multiple of 8
+  const int first = (static_cast<int>(blockIdx.x) & 7) * per_xcd;
+  const int last = min(first + per_xcd, used);
+  const int S = p.K / G::KS;
 
-  // per-row / per-column parameters (rows clamped into the routed-row arrays)
+  // Tile of work item w; false when its table entry names no tile, or a tile
+  // outside the operands (the item is skipped by the whole workgroup).
+  auto tile_of = [&](int w, int& e, int& m0, int& m_end, int& n0) -> bool {
+    const int tile = w / ncol, ct = w - tile * ncol;
+    e = p.tiles[4 * tile];
+    m0 = p.tiles[4 * tile + 1];
+    m_end = p.tiles[4 * tile + 2];
+    n0 = ct * G::BN;
+    return e >= 0 && e < p.n_experts && m0 >= 0 && m0 < p.M && m_end > m0 && m_end <= p.M;
+  };
+  int e = 0, m0 = 0, m_end = 0, n0 = 0;
+  int item = first + (static_cast<int>(blockIdx.x) >> 3);
+  while (item < last && !tile_of(item, e, m0, m_end, n0)) item += slots;
+  if (item >= last) return;
+
+  // per-row / per-column parameters of a tile (rows clamped into the
+  // routed-row arrays), held in registers until the tile's main loop parks them
   float ld_sa = 0.0f, ld_sb = 0.0f, ld_rw = 0.0f;
   int ld_dst = -1;
-  if (tid < G::BM) {
-    const int r = min(m0 + tid, p.M - 1);
-    const int src = p.row_token ? min(max(p.row_token[r], 0), p.a_rows - 1) : min(r, p.a_rows - 1);
-    if constexpr (MOE != QG_MOE_EPI_I32) ld_sa = p.a_scale[src];
-    if constexpr (MOE == QG_MOE_EPI_ROUTE) {
-      ld_rw = p.row_weight[r];
-      ld_dst = p.row_slot[r];
-    }
-  }
-  if constexpr (MOE != QG_MOE_EPI_I32) {
-    if (tid < G::BN) ld_sb = p.b_scale[static_cast<int64_t>(e) * p.N + min(n0 + tid, p.N - 1)];
-  }
-
-  const CopyPlan<4> plan(grp_x ? n0 : m0, wave & 3, lane);
-  uint32_t voff[YS];
-  static_for<0, YS>([&](auto i_c) {
-    constexpr int I = decltype(i_c)::value;
-    if (grp_x) {
-      voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, p.N - 1)) * static_cast<uint32_t>(p.w_sn) +
-                plan.chunk16;
-    } else {
-      const int r = min(plan.row0 + 32 * I, p.M - 1);
+  auto fetch_params = [&](int e_, int m0_, int n0_) __attribute__((always_inline)) {
+    if (tid < G::BM) {
+      const int r = min(m0_ + tid, p.M - 1);
       const int src = p.row_token ? min(max(p.row_token[r], 0), p.a_rows - 1) : min(r, p.a_rows - 1);
-      voff[I] = static_cast<uint32_t>(src) * static_cast<uint32_t>(p.a_sm) + plan.chunk16;
+      if constexpr (MOE != QG_MOE_EPI_I32) ld_sa = p.a_scale[src];
+      if constexpr (MOE == QG_MOE_EPI_ROUTE) {
+        ld_rw = p.row_weight[r];
+        ld_dst = p.row_slot[r];
+      }
     }
-  });
-  i32x16 acc[G::FM][G::FN];
-  static_for<0, G::FM>([&](auto i) {
-    static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
-  });
+    if constexpr (MOE != QG_MOE_EPI_I32) {
+      if (tid < G::BN) ld_sb = p.b_scale[static_cast<int64_t>(e_) * p.N + min(n0_ + tid, p.N - 1)];
+    }
+  };
+  uint32_t voff[YS];
+  auto plan_offsets = [&](int m0_, int n0_) __attribute__((always_inline)) {
+    const CopyPlan<4> plan(grp_x ? n0_ : m0_, wave & 3, lane);
+    static_for<0, YS>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      if (grp_x) {
+        voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, p.N - 1)) * static_cast<uint32_t>(p.w_sn) +
+                  plan.chunk16;
+      } else {
+        const int r = min(plan.row0 + 32 * I, p.M - 1);
+        const int src = p.row_token ? min(max(p.row_token[r], 0), p.a_rows - 1) : min(r, p.a_rows - 1);
+        voff[I] = static_cast<uint32_t>(src) * static_cast<uint32_t>(p.a_sm) + plan.chunk16;
+      }
+    });
+  };
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  auto w_base = [&](int e_) { return reinterpret_cast<const char*>(p.w) + static_cast<int64_t>(e_) * p.w_estride; };
+  fetch_params(e, m0, n0);
+  plan_offsets(m0, n0);
+
   // row scales, column scales, row weights and output rows (the latter two
   // after the GEMM's own parameter area)
   float* sa_lds = reinterpret_cast<float*>(smem + G::SC_A);
   float* sb_lds = reinterpret_cast<float*>(smem + G::SC_B);
   float* rw_lds = reinterpret_cast<float*>(smem + G::LDS_BYTES);
   int* dst_lds = reinterpret_cast<int*>(smem + G::LDS_BYTES + G::BM * 4);
-  auto park = [&]() {
-    if (tid < G::BM) {
-      sa_lds[tid] = ld_sa;
-      rw_lds[tid] = ld_rw;
-      dst_lds[tid] = ld_dst;
-    }
-    if (tid < G::BN) sb_lds[tid] = ld_sb;
-  };
-  pp_mainloop<G, MfmaI8>(acc, smem, reinterpret_cast<const char*>(p.a),
-                 reinterpret_cast<const char*>(p.w) + static_cast<int64_t>(e) * p.w_estride, voff, p.K / G::KS,
-                 wave, lane, false, park);
 
-  // ---- epilogue -------------------------------------------------------------
-  const int lr = lane & 31, lq = 4 * (lane >> 5);
-  // bf16 outputs whose rows take whole 16-byte chunks are staged per wave in
-  // its part of the rings and written as row chunks; int32 (test) output goes
+  // bf16 outputs whose rows take whole 16-byte chunks are staged per wave, 32
+  // rows at a time, and written as row chunks; int32 (test) output goes
   // element-wise
   constexpr bool STAGED = MOE != QG_MOE_EPI_I32;
   constexpr int OCOLS = MOE == QG_MOE_EPI_SILU_MUL ? G::WN / 2 : G::WN;  // output columns per wave row
   constexpr int ROWB = OCOLS * 2 + 16;
   constexpr int CH = OCOLS * 2 / 16;
-  static_assert(G::WM * ROWB <= G::RING / G::NW, "staging region");
+  static_assert(32 * ROWB <= EPI_REGION, "staging region");
+  static_assert((32 * CH) % 64 == 0, "whole chunk rounds per lane");
   const int out_cols = MOE == QG_MOE_EPI_SILU_MUL ? p.N / 2 : p.N;
+  // ST: the staged epilogue's 16-byte stores per wave and item
+  constexpr int ST = STAGED ? G::FM * (32 * CH / 64) : 0;
+  static_assert(ST + YS < 64, "vmcnt range");
+  const int64_t out_bytes = static_cast<int64_t>(p.out_rows) * p.out_sm * 2;
   const bool staged = STAGED && (out_cols % 8) == 0 && (p.out_sm % 8) == 0 &&
-                      (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
-  char* region = smem + wave * (G::RING / G::NW);
-  float sa[G::FM], rwv[G::FM];
-  static_for<0, G::FM>([&](auto i) {
-    const int rl = wr * G::WM + 32 * decltype(i)::value + lr;
-    sa[i] = sa_lds[rl];
-    rwv[i] = MOE == QG_MOE_EPI_ROUTE ? rw_lds[rl] : 0.0f;
-  });
-  static_for<0, G::FN>([&](auto j_c) {
-    constexpr int j = decltype(j_c)::value;
-    if constexpr (MOE == QG_MOE_EPI_I32) {
-      static_for<0, 4>([&](auto g_c) {
-        constexpr int g = decltype(g_c)::value;
-        static_for<0, G::FM>([&](auto i) {
-          const int row = m0 + wr * G::WM + 32 * decltype(i)::value + lr;
-          static_for<0, 4>([&](auto c) {
-            const int n = n0 + wc * G::WN + 32 * j + 8 * g + lq + decltype(c)::value;
-            if (row < m_end && n < p.N)
-              static_cast<int32_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + n] =
-                  acc[i][j][4 * g + decltype(c)::value];
-          });
-        });
-      });
-    } else if constexpr (MOE == QG_MOE_EPI_SILU_MUL) {
-      static_for<0, 2>([&](auto g_c) {
-        constexpr int g = decltype(g_c)::value;
-        const f32x4 sbg = col4(sb_lds, wc * G::WN + 32 * j + 8 * g + lq);
-        const f32x4 sbu = col4(sb_lds, wc * G::WN + 32 * j + 8 * (g + 2) + lq);
-        static_for<0, G::FM>([&](auto i) {
-          float h[4];
-          static_for<0, 4>([&](auto c) {
-            constexpr int C = decltype(c)::value;
-            const float gv = static_cast<float>(acc[i][j][4 * g + C]) * (sa[i] * sbg[C]);
-            const float uv = static_cast<float>(acc[i][j][4 * (g + 2) + C]) * (sa[i] * sbu[C]);
-            h[C] = silu(gv) * uv;
-          });
-          const int rw_ = 32 * decltype(i)::value + lr;  // row in the wave sub-tile
-          const int fl = 16 * j + 8 * g + lq;            // feature in the wave's output columns
-          if (staged) {
-            *reinterpret_cast<u32x2*>(region + rw_ * ROWB + fl * 2) =
-                u32x2{pack2<QG_BF16>(h[0], h[1]), pack2<QG_BF16>(h[2], h[3])};
-          } else {
-            const int row = m0 + wr * G::WM + rw_;
-            const int f0 = (n0 + wc * G::WN) / 2 + fl;
-            if (row < m_end) {
-              static_for<0, 4>([&](auto c) {
-                if (f0 + decltype(c)::value < out_cols)
-                  static_cast<uint16_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + f0 + decltype(c)::value] =
-                      f32_to_bf16(h[decltype(c)::value]);
-              });
-            }
-          }
-        });
-      });
-    } else {
-      static_for<0, 4>([&](auto g_c) {
-        constexpr int g = decltype(g_c)::value;
-        const int cl = wc * G::WN + 32 * j + 8 * g + lq;  // tile column
-        const f32x4 sb4 = col4(sb_lds, cl);
-        static_for<0, G::FM>([&](auto i) {
-          float y[4];
-          static_for<0, 4>([&](auto c) {
-            constexpr int C = decltype(c)::value;
-            const float v = static_cast<float>(acc[i][j][4 * g + C]) * (sa[i] * sb4[C]);
-            y[C] = v * rwv[i];
-          });
-          const int rw_ = 32 * decltype(i)::value + lr;
-          if (staged) {
-            *reinterpret_cast<u32x2*>(region + rw_ * ROWB + (32 * j + 8 * g + lq) * 2) =
-                u32x2{pack2<QG_BF16>(y[0], y[1]), pack2<QG_BF16>(y[2], y[3])};
-          } else {
-            const int rl = wr * G::WM + rw_;
-            const int d = dst_lds[rl];
-            if (m0 + rl < m_end && d >= 0 && d < p.out_rows) {
-              static_for<0, 4>([&](auto c) {
-                const int n = n0 + cl + decltype(c)::value;
-                if (n < p.N)
-                  static_cast<uint16_t*>(p.out)[static_cast<int64_t>(d) * p.out_sm + n] =
-                      f32_to_bf16(y[decltype(c)::value]);
-              });
-            }
-          }
-        });
-      });
+                      (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && out_bytes <= kOobOffset;
+  // raw buffer over out (num_records in bytes, below kOobOffset)
+  const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      p.out, 0, static_cast<int>(staged ? out_bytes : 0), kBufferWord3);
+  char* const region = smem + EPI_BASE + wave * EPI_REGION;
+
+  bool pre = false;
+  i32x16 acc[G::FM][G::FN];
+  for (;;) {
+    // lane-derived offsets recomputed per item instead of hoisted (registers)
+    int lane_t = lane;
+    asm volatile("" : "+v"(lane_t));
+    static_for<0, G::FM>([&](auto i) {
+      static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
+    });
+    auto park = [&]() __attribute__((always_inline)) {
+      if (tid < G::BM) {
+        sa_lds[tid] = ld_sa;
+        rw_lds[tid] = ld_rw;
+        dst_lds[tid] = ld_dst;
+      }
+      if (tid < G::BN) sb_lds[tid] = ld_sb;
+    };
+    pp_mainloop<G, MfmaI8, ST>(acc, smem, a_base, w_base(e), voff, S, wave, lane_t, pre, park, staged);
+
+    // the next item: its table entry, parameters, copy offsets and stage-0
+    // copies, ahead of this item's epilogue. The parameters come first: their
+    // row gathers wait for loads, which would also wait for copies issued
+    // before them.
+    int nitem = item + slots;
+    int e1 = 0, m1 = 0, mend1 = 0, n1 = 0;
+    while (nitem < last && !tile_of(nitem, e1, m1, mend1, n1)) nitem += slots;
+    const bool more = nitem < last;
+    if (more) {
+      fetch_params(e1, m1, n1);
+      plan_offsets(m1, n1);
+      if (S > 0) pp_prefetch0<G>(smem, a_base, w_base(e1), voff, wave);
     }
-  });
-  if constexpr (STAGED) {
-    if (staged) {
-      // LDS accesses of one wave complete in order: the reads see the writes
-      const int col0 = (MOE == QG_MOE_EPI_SILU_MUL ? (n0 + wc * G::WN) / 2 : n0 + wc * G::WN);
-      for (int c = lane; c < G::WM * CH; c += 64) {
-        const int rr = c / CH, cc = c - rr * CH;
-        const int rl = wr * G::WM + rr;
-        const int row = m0 + rl;
-        const int d = MOE == QG_MOE_EPI_ROUTE ? dst_lds[rl] : row;
-        const int col = col0 + cc * 8;
-        if (row < m_end && d >= 0 && d < p.out_rows && col + 8 <= out_cols) {
-          const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
-          *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(p.out) + static_cast<int64_t>(d) * p.out_sm + col) = v;
+
+    // ---- epilogue of this item ----------------------------------------------
+    const int lr = lane_t & 31, lq = 4 * (lane_t >> 5);
+    static_for<0, G::FM>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      const int rl_i = wr * G::WM + 32 * i + lr;  // row in the tile
+      const float sa = sa_lds[rl_i];
+      const float rwv = MOE == QG_MOE_EPI_ROUTE ? rw_lds[rl_i] : 0.0f;
+      static_for<0, G::FN>([&](auto j_c) {
+        constexpr int j = decltype(j_c)::value;
+        if constexpr (MOE == QG_MOE_EPI_I32) {
+          static_for<0, 4>([&](auto g_c) {
+            constexpr int g = decltype(g_c)::value;
+            const int row = m0 + rl_i;
+            static_for<0, 4>([&](auto c) {
+              const int n = n0 + wc * G::WN + 32 * j + 8 * g + lq + decltype(c)::value;
+              if (row < m_end && n < p.N)
+                static_cast<int32_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + n] =
+                    acc[i][j][4 * g + decltype(c)::value];
+            });
+          });
+        } else if constexpr (MOE == QG_MOE_EPI_SILU_MUL) {
+          static_for<0, 2>([&](auto g_c) {
+            constexpr int g = decltype(g_c)::value;
+            const f32x4 sbg = col4(sb_lds, wc * G::WN + 32 * j + 8 * g + lq);
+            const f32x4 sbu = col4(sb_lds, wc * G::WN + 32 * j + 8 * (g + 2) + lq);
+            float h[4];
+            static_for<0, 4>([&](auto c) {
+              constexpr int C = decltype(c)::value;
+              const float gv = static_cast<float>(acc[i][j][4 * g + C]) * (sa * sbg[C]);
+              const float uv = static_cast<float>(acc[i][j][4 * (g + 2) + C]) * (sa * sbu[C]);
+              h[C] = silu(gv) * uv;
+            });
+            const int fl = 16 * j + 8 * g + lq;  // feature in the wave's output columns
+            if (staged) {
+              *reinterpret_cast<u32x2*>(region + lr * ROWB + fl * 2) =
+                  u32x2{pack2<QG_BF16>(h[0], h[1]), pack2<QG_BF16>(h[2], h[3])};
+            } else {
+              const int row = m0 + rl_i;
+              const int f0 = (n0 + wc * G::WN) / 2 + fl;
+              if (row < m_end) {
+                static_for<0, 4>([&](auto c) {
+                  if (f0 + decltype(c)::value < out_cols)
+                    static_cast<uint16_t*>(p.out)[static_cast<int64_t>(row) * p.out_sm + f0 + decltype(c)::value] =
+                        f32_to_bf16(h[decltype(c)::value]);
+                });
+              }
+            }
+          });
+        } else {
+          static_for<0, 4>([&](auto g_c) {
+            constexpr int g = decltype(g_c)::value;
+            const int cl = wc * G::WN + 32 * j + 8 * g + lq;  // tile column
+            const f32x4 sb4 = col4(sb_lds, cl);
+            float y[4];
+            static_for<0, 4>([&](auto c) {
+              constexpr int C = decltype(c)::value;
+              const float v = static_cast<float>(acc[i][j][4 * g + C]) * (sa * sb4[C]);
+              y[C] = v * rwv;
+            });
+            if (staged) {
+              *reinterpret_cast<u32x2*>(region + lr * ROWB + (32 * j + 8 * g + lq) * 2) =
+                  u32x2{pack2<QG_BF16>(y[0], y[1]), pack2<QG_BF16>(y[2], y[3])};
+            } else {
+              const int d = dst_lds[rl_i];
+              if (m0 + rl_i < m_end && d >= 0 && d < p.out_rows) {
+                static_for<0, 4>([&](auto c) {
+                  const int n = n0 + cl + decltype(c)::value;
+                  if (n < p.N)
+                    static_cast<uint16_t*>(p.out)[static_cast<int64_t>(d) * p.out_sm + n] =
+                        f32_to_bf16(y[decltype(c)::value]);
+                });
+              }
+            }
+          });
+        }
+      });
+      if constexpr (STAGED) {
+        if (staged) {
+          // LDS accesses of one wave complete in order: the reads see this
+          // pass's writes, and the next pass's writes follow these reads
+          const int col0 = (MOE == QG_MOE_EPI_SILU_MUL ? (n0 + wc * G::WN) / 2 : n0 + wc * G::WN);
+#pragma unroll
+          for (int c0 = 0; c0 < 32 * CH; c0 += 64) {
+            const int c = c0 + lane_t;
+            const int rr = c / CH, cc = c - rr * CH;
+            const int rl = wr * G::WM + 32 * i + rr;
+            const int row = m0 + rl;
+            const int d = MOE == QG_MOE_EPI_ROUTE ? dst_lds[rl] : row;
+            const int col = col0 + cc * 8;
+            const bool ok = row < m_end && d >= 0 && d < p.out_rows && col + 8 <= out_cols;
+            const uint32_t off = ok ? static_cast<uint32_t>((static_cast<int64_t>(d) * p.out_sm + col) * 2) : kOobOffset;
+            const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
+            __builtin_amdgcn_raw_buffer_store_b128(v, out_rsrc, off, 0, 0);
+          }
         }
       }
-    }
+    });
+    if (!more) break;
+    wait_lds_barrier();
+    item = nitem;
+    e = e1;
+    m0 = m1;
+    m_end = mend1;
+    n0 = n1;
+    pre = S > 0;
   }
 }
 
@@ -1290,8 +1356,10 @@ hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream) {
   // 192-row tiles: expert segments of ~512-576 rows (cfg4) fill 3 tiles
   using G = I8Geo<QG_MOE_TILE_ROWS, 256, 2, 4, 3>;
   static_assert(G::LDS_BYTES <= 160 * 1024, "LDS per CU");
-  const int blocks = p.tiles_max * ceil_div(p.N, G::BN);
-  if (blocks == 0) return hipSuccess;
+  // persistent: at most one workgroup per CU, a multiple of the 8 XCDs
+  const long items = static_cast<long>(p.tiles_max) * ceil_div(p.N, G::BN);
+  if (items == 0) return hipSuccess;
+  const int blocks = items < kPersistentCUs ? static_cast<int>((items + 7) & ~7L) : kPersistentCUs;
   switch (p.moe_epi) {
     case QG_MOE_EPI_I32:
       hipLaunchKernelGGL((k_i8_moe_pp<G, QG_MOE_EPI_I32>), dim3(blocks), dim3(G::THREADS), 0, stream, p);

@@ -185,3 +185,99 @@ def test_moe_dispatch_no_tokens(cuda):
     prep = m.prepare_moe_weights(wg.to(cuda), wu.to(cuda), wd.to(cuda))
     out = m.moe_int8_forward(x[:0].to(cuda), logits[:0].to(cuda), prep, top_k=k)
     assert out.shape == (0, 128) and out.dtype == torch.bfloat16
+
+
+def _grouped_call(cuda, a, w, tiles, a_scale, b_scale, row_weight, row_slot, epi, out):
+    """qg_moe_grouped_gemm on explicit operands (row_token NULL: routed row r
+    is a's row r); out is written in place."""
+    from rdna2_ops import _lib
+    e, n, k = w.shape
+    P = _lib.ptr
+    _lib.check(_lib.library().qg_moe_grouped_gemm(
+        P(a), a.stride(0), a.shape[0], None, a.shape[0], k, P(w), k, n * k, n, e, P(tiles), tiles.shape[0],
+        P(a_scale) if a_scale is not None else None, P(b_scale) if b_scale is not None else None,
+        P(row_weight) if row_weight is not None else None, P(row_slot) if row_slot is not None else None,
+        epi, P(out), out.stride(0), out.shape[0], _lib.stream_of(a)), "qg_moe_grouped_gemm")
+
+
+def test_moe_grouped_table_skips_and_output_strides(cuda):
+    """The grouped GEMM's walk of a hand-made tile table: entries in use that
+    name no expert (-1) or an expert past n_experts are skipped, as is a valid
+    entry past the count in use; partial tiles stop at their valid rows; route
+    targets of -1 or past the slot count are not written. Each epilogue runs
+    with an output row stride that takes the staged 16-byte stores (a multiple
+    of 8) and one that takes the element-wise stores; both give the same bits,
+    every write lands where the oracle puts it (int32 and route bit-exact, h
+    within the SiLU's fp32 error plus one bf16 rounding), and nothing else in
+    the output changes."""
+    from rdna2_ops import _lib
+    case("moe grouped GEMM tile table skips, output strides")
+    rng = np.random.default_rng(5)
+    E, K, N, M = 4, 256, 256, 576
+    a = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-127, 128, (E, N, K), dtype=np.int8)
+    sa = (rng.random(M, dtype=np.float32) * 0.02 + 0.001).astype(np.float32)
+    sb = (rng.random((E, N), dtype=np.float32) * 0.02 + 0.001).astype(np.float32)
+    rw = rng.random(M, dtype=np.float32).astype(np.float32)
+    slot = rng.permutation(M).astype(np.int32)
+    slot[[3, 200, 400, 575]] = -1
+    slot[[10, 390]] = M  # past the slot count
+    tiles = np.array([[0, 0, 150, 5], [-1, 150, 190, 0], [2, 192, 300, 0], [7, 300, 380, 0],
+                      [1, 384, 576, 0], [3, 0, 10, 0]], np.int32)
+    valid = [(0, 0, 150), (2, 192, 300), (1, 384, 576)]  # (expert, first row, end)
+    acc = np.zeros((M, N), np.int64)
+    for e, r0, r1 in valid:
+        acc[r0:r1] = a[r0:r1].astype(np.int64) @ w[e].T.astype(np.int64)
+    d = {k_: torch.from_numpy(v).to(cuda) for k_, v in
+         dict(a=a, w=w, sa=sa, sb=sb, rw=rw, slot=slot, tiles=tiles).items()}
+
+    # int32 products (element-wise stores), rows outside the valid tiles untouched
+    out = torch.full((M, N), -7, dtype=torch.int32, device=cuda)
+    _grouped_call(cuda, d["a"], d["w"], d["tiles"], None, None, None, None, _lib.MOE_EPI_I32, out)
+    got = out.cpu().numpy()
+    exp = np.full((M, N), -7, np.int64)
+    for e, r0, r1 in valid:
+        exp[r0:r1] = acc[r0:r1]
+    assert np.array_equal(got.astype(np.int64), exp)
+
+    # route epilogue: y[slot[r]] = bf16((f32(acc) * (sa * sb)) * rw), staged and element-wise
+    exp_y = np.full((M, N), np.nan, np.float32)
+    for e, r0, r1 in valid:
+        yv = om.down(a[r0:r1], sa[r0:r1], w[e], sb[e], rw[r0:r1])
+        for i, r in enumerate(range(r0, r1)):
+            if 0 <= slot[r] < M:
+                exp_y[slot[r]] = yv[i]
+    outs = []
+    for pad in (0, 3):
+        buf = torch.full((M, N + pad), -1, dtype=torch.int16, device=cuda)  # 0xFFFF: a bf16 NaN
+        y = buf.view(torch.bfloat16)
+        _grouped_call(cuda, d["a"], d["w"], d["tiles"], d["sa"], d["sb"], d["rw"], d["slot"], _lib.MOE_EPI_ROUTE, y)
+        bits = buf.cpu().numpy()
+        assert (bits[:, N:] == -1).all(), f"route pad {pad}: row padding written"
+        vals = y[:, :N].float().cpu().numpy()
+        hit = ~np.isnan(exp_y)
+        assert np.array_equal(vals[hit], exp_y[hit]), f"route pad {pad}"
+        assert (bits[:, :N][~hit] == -1).all(), f"route pad {pad}: rows without a valid target written"
+        outs.append(bits[:, :N])
+    assert np.array_equal(outs[0], outs[1])
+
+    # SiLU * mul epilogue: gate rows 32 b .. + 15, up rows 32 b + 16 .. + 31
+    F = N // 2
+    g_rows = np.array([32 * (f // 16) + f % 16 for f in range(F)])
+    outs = []
+    for pad in (0, 1):
+        buf = torch.full((M, F + pad), -1, dtype=torch.int16, device=cuda)
+        h = buf.view(torch.bfloat16)
+        _grouped_call(cuda, d["a"], d["w"], d["tiles"], d["sa"], d["sb"], None, None, _lib.MOE_EPI_SILU_MUL, h)
+        bits = buf.cpu().numpy()
+        assert (bits[:, F:] == -1).all(), f"silu pad {pad}: row padding written"
+        vals = h[:, :F].float().cpu().numpy()
+        written = np.zeros(M, bool)
+        for e, r0, r1 in valid:
+            written[r0:r1] = True
+            ref = om.gate_up(a[r0:r1], sa[r0:r1], w[e][g_rows], sb[e][g_rows], w[e][g_rows + 16], sb[e][g_rows + 16])
+            err = np.abs(vals[r0:r1] - ref)
+            assert (err <= 2.0 ** -7 * np.abs(ref) + 1e-6).all(), (f"silu pad {pad}", e, err.max())
+        assert (bits[~written][:, :F] == -1).all(), f"silu pad {pad}: rows outside the tiles written"
+        outs.append(bits[:, :F])
+    assert np.array_equal(outs[0], outs[1])

@@ -15,7 +15,9 @@ before timing; weights are synthetic N(0, 0.02) quantized per output channel.
 Prints one JSON line (driver contract). ``value`` = whole-chain TOPS
 (2*M*N*K summed over the three GEMMs, divided by the step time).
 ``roofline`` covers the dominant kernel (the int8 GEMM), timed with HIP events
-around each GEMM launch on its stream inside the timed steps.
+around each GEMM launch on the chain's stream in instrumented chain rounds,
+alternated with the plain rounds that give ``value`` (the event records add
+about 4 % to a step).
 ``roofline_w4a16_decode`` is the metric's second half: the W4A16 decode kernel
 (M = 1) in GB/s against the 8 TB/s HBM peak, timed
 with events around graph replays of 120 launches over 12 rotated weight copies;
@@ -27,8 +29,9 @@ W4A16 M = 16 / 2048, the FP8 configuration 3, MoE (configuration 4) and W4A8.
 
 Timing protocol (the reference's, rdna2-ops/bench_int8_gemm.py:259-268):
 --rounds alternating rounds (forward order on even rounds, reverse on odd) of
-the chain (exactly --steps steps per round between synchronisations), the
-cfg0 GEMM and quantizer and the two decode shapes; every figure is the median
+the chain (exactly --steps steps per round between synchronisations; a plain
+and an instrumented round each), the cfg0 GEMM and quantizer and the two
+decode shapes; every figure is the median
 over rounds, the per-round samples are reported. ``clock`` is the GPU's GFX
 clock read with amdsmi over a 2.5 s window of the same chain after the rounds.
 """
@@ -76,7 +79,7 @@ def parse():
 class Chain:
     """Preallocated buffers and direct C-ABI launches of the cfg1 chain."""
 
-    def __init__(self, torch, lib, _lib, quantize, cfg, dev):
+    def __init__(self, torch, lib, _lib, quantize, cfg, dev, stream=None):
         self.t, self.lib, self.L = torch, lib, _lib
         self.m = cfg.x.shape[0]
         self.x = cfg.x.to(dev)
@@ -90,7 +93,7 @@ class Chain:
                 xq=torch.empty((self.m, k), dtype=torch.int8, device=dev),
                 xs=torch.empty((self.m,), dtype=torch.float32, device=dev),
                 out=torch.empty((self.m, n), dtype=torch.float16, device=dev)))
-        self.stream = torch.cuda.current_stream(dev)
+        self.stream = stream if stream is not None else torch.cuda.current_stream(dev)
         self.s = self.stream.cuda_stream
         self.inputs = [self.x, self.x, self.layers[1]["out"]]
 
@@ -637,36 +640,44 @@ def main():
         res = runs[args.only]()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return
-    chain = Chain(torch, lib, _lib, quantize_int8_rowwise, synthetic.cfg1(), dev)
+    # the chain runs on a stream of its own (default priority)
+    chain_stream = torch.cuda.Stream(device=dev)
+    chain = Chain(torch, lib, _lib, quantize_int8_rowwise, synthetic.cfg1(), dev, stream=chain_stream)
     for _ in range(args.warmup):
         chain.step()
     torch.cuda.synchronize()
 
     events = []
 
-    def chain_round():
+    def chain_round(instrumented):
         """Exactly --steps chain steps between two synchronisations; ms per step.
-        The per-GEMM timing events are created before the timed region and the
-        garbage collector is paused inside it: creating events there made the
-        host, not the GPU, the bottleneck of one round in several (host enqueue
-        0.77 ms per step against 0.04)."""
+        Instrumented rounds bracket every GEMM launch with a pair of timing
+        events (the roofline's per-launch durations); the plain rounds give
+        ``value``: the six event records per step cost about 16 us of a
+        ~430 us step (measured on MI355X, same process). The events are created
+        before the timed region and the garbage collector is paused inside it:
+        creating events there made the host, not the GPU, the bottleneck of one
+        round in several (host enqueue 0.77 ms per step against 0.04)."""
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
         pairs = iter([(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                      for _ in range(3 * args.steps)])
+                      for _ in range(3 * args.steps)]) if instrumented else None
         torch.cuda.synchronize()
         gc.disable()
         try:
             start.record(chain.stream)
             for _ in range(args.steps):
-                chain.step(events, pairs)
+                if instrumented:
+                    chain.step(events, pairs)
+                else:
+                    chain.step()
             stop.record(chain.stream)
             torch.cuda.synchronize()
         finally:
             gc.enable()
         return start.elapsed_time(stop) / args.steps
 
-    items = {"chain": chain_round}
+    items = {"chain": lambda: chain_round(False), "chain_gemm_events": lambda: chain_round(True)}
     cfg0 = decode = None
     if not args.no_secondary:
         cfg0 = Cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev)
@@ -706,7 +717,11 @@ def main():
                    "tokens": chain.m, "hidden": 3072, "ops_per_step": ops},
         "protocol": {"rounds": args.rounds, "order": "alternating (forward on even rounds, reverse on odd)",
                      "statistic": "median over rounds", "steps_per_round": args.steps,
-                     "chain_ms_per_step_by_round": [round(v, 5) for v in chain_samples]},
+                     "chain_ms_per_step_by_round": [round(v, 5) for v in chain_samples],
+                     "value_from": "plain chain rounds (no events between launches)",
+                     "roofline_from": "instrumented chain rounds (an event pair around every GEMM launch on "
+                                      "the chain's stream), alternated with the plain rounds",
+                     "instrumented_chain_ms_per_step_by_round": [round(v, 5) for v in timed["chain_gemm_events"][1]]},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS,
                      "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,

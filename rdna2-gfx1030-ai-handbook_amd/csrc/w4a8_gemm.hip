@@ -89,7 +89,7 @@ struct WStage {
   uint32_t zb[4];
 };
 
-template <int G, bool PREP, bool INTEGER, int NW>
+template <int G, bool PREP, bool INTEGER, int NW, bool VEC>
 __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
 #pragma clang fp contract(off)
   constexpr int GK = G / 32;      // k-steps per group
@@ -152,10 +152,20 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
       if constexpr (PREP) {
         const i32x4 v = *reinterpret_cast<const i32x4*>(p.w8 + static_cast<int64_t>(nw) * p.w8_sn + kt * 32 + 16 * h);
         static_for<0, 4>([&](auto e) { b.w[t][e] = static_cast<uint32_t>(v[decltype(e)::value]); });
-      } else {
+      } else if constexpr (!VEC) {
         const int64_t j = 4 * kt + 2 * h;
         b.w[t][0] = wrow[j * kstride];
         b.w[t][1] = wrow[(j + 1) * kstride];
+      } else if constexpr (t < 2) {
+        // nk rows, 16-byte aligned: two 16-byte loads per lane and stage (words
+        // 16 s + 4 h + 8 t .. + 3 of the lane's row, clamped into the row: a
+        // clamped load only feeds k-steps past K), regrouped in compute()
+        const int o = min(16 * s + 4 * h + 8 * t, p.K / 8 - 4);
+        const i32x4 v = *reinterpret_cast<const i32x4*>(wrow + o);
+        b.w[2 * t][0] = static_cast<uint32_t>(v[0]);
+        b.w[2 * t][1] = static_cast<uint32_t>(v[1]);
+        b.w[2 * t + 1][0] = static_cast<uint32_t>(v[2]);
+        b.w[2 * t + 1][1] = static_cast<uint32_t>(v[3]);
       }
     });
     if constexpr (!PREP) {
@@ -233,9 +243,31 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
   };
 
   // MFMAs of stage s (A in slot s & 1, weights in b).
-  auto compute = [&](int s, const WStage<PREP>& b) __attribute__((always_inline)) {
+  auto compute = [&](int s, const WStage<PREP>& b_in) __attribute__((always_inline)) {
     const int slot = s & 1;
     const char* abase = smem + slot * kSlotA;
+    // VEC: lane half h loaded words 4 h .. 4 h + 3 and 8 + 4 h .. 11 + 4 h of
+    // the stage (b_in.w[0..3] = those 8 words in order); k-step t needs words
+    // 4 t + 2 h, + 1. Each half keeps the pairs it holds and swaps the other
+    // two with the lane 32 away.
+    WStage<PREP> b = b_in;
+    if constexpr (VEC) {
+      const uint32_t* r = &b_in.w[0][0];  // r[0..3] = first load, r[4..7] = second
+      uint32_t snd[4], got[4];
+      snd[0] = h ? r[0] : r[2];
+      snd[1] = h ? r[1] : r[3];
+      snd[2] = h ? r[4] : r[6];
+      snd[3] = h ? r[5] : r[7];
+      static_for<0, 4>([&](auto i) { got[i] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(snd[i]), 32, 64)); });
+      b.w[0][0] = h ? got[0] : r[0];
+      b.w[0][1] = h ? got[1] : r[1];
+      b.w[1][0] = h ? r[2] : got[0];
+      b.w[1][1] = h ? r[3] : got[1];
+      b.w[2][0] = h ? got[2] : r[4];
+      b.w[2][1] = h ? got[3] : r[5];
+      b.w[3][0] = h ? r[6] : got[2];
+      b.w[3][1] = h ? r[7] : got[3];
+    }
     static_for<0, 4>([&](auto t_c) {
       constexpr int t = decltype(t_c)::value;
       if (s * 4 + t < KT) {
@@ -357,10 +389,17 @@ template <int G, bool PREP>
 hipError_t launch_g(const W4A8Args& p, hipStream_t stream) {
   constexpr int NW = kW4A8Waves;
   const int blocks = ceil_div(p.M, kBM) * ceil_div(p.N, W8Geo<NW>::BN);
-  if (p.integer)
-    hipLaunchKernelGGL((k_w4a8<G, PREP, true, NW>), dim3(blocks), dim3(W8Geo<NW>::THREADS), 0, stream, p);
-  else
-    hipLaunchKernelGGL((k_w4a8<G, PREP, false, NW>), dim3(blocks), dim3(W8Geo<NW>::THREADS), 0, stream, p);
+  // nk words with 16-byte aligned rows (K % 32 == 0 makes every row a
+  // multiple of 16 bytes): 16-byte weight loads
+  const bool vec = !PREP && !(p.flags & QG_W4_LAYOUT_KN) && (reinterpret_cast<uintptr_t>(p.w) & 15) == 0;
+  const dim3 grid(blocks), block(W8Geo<NW>::THREADS);
+  if (p.integer) {
+    if (vec) hipLaunchKernelGGL((k_w4a8<G, PREP, true, NW, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((k_w4a8<G, PREP, true, NW, false>), grid, block, 0, stream, p);
+  } else {
+    if (vec) hipLaunchKernelGGL((k_w4a8<G, PREP, false, NW, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((k_w4a8<G, PREP, false, NW, false>), grid, block, 0, stream, p);
+  }
   return hipGetLastError();
 }
 

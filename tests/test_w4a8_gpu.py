@@ -72,12 +72,14 @@ def test_w4a8_formats(cuda, g, sym, layout, order):
 
 
 @pytest.mark.parametrize("m,n,k,g", [(37, 53, 384, 32), (129, 130, 256, 64), (1, 7, 96, 32), (65, 200, 192, 64),
-                                     (300, 140, 320, 64), (5, 129, 640, 128)])
-def test_w4a8_shapes_and_tails(cuda, m, n, k, g):
-    """Row / column tails, a single row, K = 96, 192, 320, 640 (last stage of
-    128 K partly or not at all filled)."""
-    case(f"w4a8 shape {m}x{n}x{k} g{g}")
-    p, c, s, a, sa, bias = make(cuda, m, n, k, g, layout="kn", seed=m + n)
+                                     (300, 140, 320, 64), (5, 129, 640, 128), (33, 70, 352, 32), (17, 90, 160, 32)])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_w4a8_shapes_and_tails(cuda, m, n, k, g, layout):
+    """Row / column tails, a single row, K = 96, 160, 192, 320, 352, 640 (last
+    stage of 128 K filled by 1, 2 or 3 of its 4 k-steps, or whole); nk words
+    take the kernel's 16-byte weight loads, kn words 4-byte loads."""
+    case(f"w4a8 shape {m}x{n}x{k} g{g} {layout}")
+    p, c, s, a, sa, bias = make(cuda, m, n, k, g, layout=layout, seed=m + n)
     check(cuda, p, c, s, a, sa, bias, g, f"{m}x{n}x{k}")
 
 

@@ -390,6 +390,22 @@ int qg_moe_dispatch(const float* logits, int64_t l_sm, int64_t tokens, int n_exp
                     float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,
                     int64_t tiles_max, void* stream);
 
+/* qg_moe_dispatch that also quantizes x for the gate/up GEMM, in the same
+ * routing launch: x bf16 [tokens, hidden] (row stride x_sm elements, 16-byte
+ * aligned rows) -> xq int8 (row stride xq_sm, 8-byte aligned rows) and xs
+ * fp32 [tokens], bit-identical to qg_quant_rows_i8(x, QG_BF16, ...,
+ * QG_ROUND_HALF_EVEN). hidden % 8 == 0 and hidden <= 2048 (one wave per token
+ * holds its row); anything else returns hipErrorInvalidValue and the caller
+ * runs qg_moe_dispatch and qg_quant_rows_i8. This build's own (BASELINE
+ * configuration 4 has no counterpart in the reference): the quantization's
+ * loads overlap the routing's latency-bound shuffles instead of a launch of
+ * their own. */
+int qg_moe_dispatch_qx(const float* logits, int64_t l_sm, int64_t tokens, int n_experts, int top_k, int pad,
+                       int32_t* experts, float* weights, int32_t* counts, int32_t* row_token,
+                       float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,
+                       int64_t tiles_max, const void* x, int64_t x_sm, int64_t hidden, int8_t* xq,
+                       int64_t xq_sm, float* xs, void* stream);
+
 /* Grouped INT8 GEMM over the dispatch's tile table: for each routed row r of
  * expert e, acc[r, n] = sum_k a[src(r), k] * w[e, n, k] with src(r) =
  * row_token[r] (row_token NULL: r itself), then the epilogue. a: int8

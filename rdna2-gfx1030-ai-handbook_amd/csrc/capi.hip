@@ -782,10 +782,13 @@ extern "C" int qg_moe_sizes(int64_t tokens, int n_experts, int top_k, int pad, i
   return moe_sizes(tokens, n_experts, top_k, pad, rows_max, tiles_max) ? hipSuccess : hipErrorInvalidValue;
 }
 
-extern "C" int qg_moe_dispatch(const float* logits, int64_t l_sm, int64_t tokens, int n_experts, int top_k,
-                               int pad, int32_t* experts, float* weights, int32_t* counts, int32_t* row_token,
-                               float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,
-                               int64_t tiles_max, void* stream) {
+namespace {
+
+// Argument checks and arguments of qg_moe_dispatch (x fields left empty).
+hipError_t moe_dispatch_args(const float* logits, int64_t l_sm, int64_t tokens, int n_experts, int top_k, int pad,
+                             int32_t* experts, float* weights, int32_t* counts, int32_t* row_token,
+                             float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,
+                             int64_t tiles_max, qg::MoeDispatchArgs* out) {
   int64_t need_rows = 0, need_tiles = 0;
   if (!moe_sizes(tokens, n_experts, top_k, pad, &need_rows, &need_tiles)) return hipErrorInvalidValue;
   if (rows_max < need_rows || tiles_max < need_tiles || rows_max >= (int64_t(1) << 30) ||
@@ -811,6 +814,45 @@ extern "C" int qg_moe_dispatch(const float* logits, int64_t l_sm, int64_t tokens
   p.tiles = tiles;
   p.tiles_max = static_cast<int>(tiles_max);
   p.tile_rows = QG_MOE_TILE_ROWS;
+  *out = p;
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int qg_moe_dispatch(const float* logits, int64_t l_sm, int64_t tokens, int n_experts, int top_k,
+                               int pad, int32_t* experts, float* weights, int32_t* counts, int32_t* row_token,
+                               float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,
+                               int64_t tiles_max, void* stream) {
+  qg::MoeDispatchArgs p{};
+  const hipError_t e = moe_dispatch_args(logits, l_sm, tokens, n_experts, top_k, pad, experts, weights, counts,
+                                         row_token, row_weight, row_slot, rows_max, tiles, tiles_max, &p);
+  if (e != hipSuccess) return e;
+  return qg::launch_moe_dispatch(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qg_moe_dispatch_qx(const float* logits, int64_t l_sm, int64_t tokens, int n_experts, int top_k,
+                                  int pad, int32_t* experts, float* weights, int32_t* counts, int32_t* row_token,
+                                  float* row_weight, int32_t* row_slot, int64_t rows_max, int32_t* tiles,
+                                  int64_t tiles_max, const void* x, int64_t x_sm, int64_t hidden, int8_t* xq,
+                                  int64_t xq_sm, float* xs, void* stream) {
+  qg::MoeDispatchArgs p{};
+  const hipError_t e = moe_dispatch_args(logits, l_sm, tokens, n_experts, top_k, pad, experts, weights, counts,
+                                         row_token, row_weight, row_slot, rows_max, tiles, tiles_max, &p);
+  if (e != hipSuccess) return e;
+  if (hidden <= 0 || hidden % 8 != 0 || hidden > qg::kMoeRouteQuantMaxH || x_sm < hidden || x_sm % 8 != 0 ||
+      xq_sm < hidden || xq_sm % 8 != 0)
+    return hipErrorInvalidValue;
+  if (tokens > 0 && (!x || !xq || !xs || (reinterpret_cast<uintptr_t>(x) & 15) != 0 ||
+                     (reinterpret_cast<uintptr_t>(xq) & 7) != 0))
+    return hipErrorInvalidValue;
+  if (tokens * x_sm >= (int64_t(1) << 40) || tokens * xq_sm >= (int64_t(1) << 40)) return hipErrorInvalidValue;
+  p.x = static_cast<const uint16_t*>(x);
+  p.x_sm = x_sm;
+  p.H = static_cast<int>(hidden);
+  p.xq = xq;
+  p.xq_sm = xq_sm;
+  p.xs = xs;
   return qg::launch_moe_dispatch(p, static_cast<hipStream_t>(stream));
 }
 

@@ -22,6 +22,7 @@
 //   combine  out[t] = bf16(sum over k of y[t * top_k + k]) in k order (fp32)
 #include "qg_common.h"
 #include "qg_internal.h"
+#include "qg_quant.h"
 
 namespace qg {
 
@@ -56,8 +57,14 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
 // counts layout: [0, E) counts, [E, 2E) segment offsets, [2E, 3E) first tile
 // of each expert, then [kMaxSortBlocks][E] per-block histograms (the
 // workspace holds (3 + 256) E ints).
+// QX: the wave also quantizes token t's row of x (the per-token activation
+// quantization of the gate/up GEMM, bit-identical to k_quant_rows_reg): its
+// loads are issued before the routing, which they overlap, and the codes are
+// formed and stored after it.
+template <bool QX>
 __global__ __launch_bounds__(kRouteWaves * 64) void k_moe_route(MoeDispatchArgs p) {
 #pragma clang fp contract(off)
+  constexpr int kQxChunks = kMoeRouteQuantMaxH / 8 / 64;  // 16-byte chunks per lane
   __shared__ int hist[64];
   const int tb = sort_block_tokens(p.T);
   const int b = blockIdx.x;
@@ -67,7 +74,22 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_moe_route(MoeDispatchArgs 
   const bool live = e < p.E;
   const int t_end = min(p.T, (b + 1) * tb);
   for (int t = b * tb + wave; t < t_end; t += kRouteWaves) {
-    const float l = live ? p.logits[static_cast<int64_t>(t) * p.l_sm + e] : -__builtin_inff();
+    // the logit of a clamped lane, replaced below: an unconditional load, so
+    // the row's loads issued after it stay in flight while the routing waits
+    // for the logit only (loads complete in order)
+    const float l_raw = p.logits[static_cast<int64_t>(t) * p.l_sm + min(e, p.E - 1)];
+    i32x4 xr[kQxChunks];
+    if constexpr (QX) {
+      asm volatile("" ::: "memory");
+      // unconditional loads of clamped chunks (a conditional load would make
+      // the compiler wait for every load at the join); chunks past the row are
+      // zeroed where they are used
+      const i32x4* row = reinterpret_cast<const i32x4*>(p.x + static_cast<int64_t>(t) * p.x_sm);
+      const int last = (p.H >> 3) - 1;
+#pragma unroll
+      for (int i = 0; i < kQxChunks; ++i) xr[i] = row[min(e + 64 * i, last)];
+    }
+    const float l = live ? l_raw : -__builtin_inff();
     const float mx = wave_max(l);
     const float ex = live ? __builtin_amdgcn_exp2f((l - mx) * 1.4426950408889634f) : 0.0f;
     const float prob = __fdiv_rn(ex, wave_sum(ex));
@@ -85,6 +107,30 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_moe_route(MoeDispatchArgs 
         p.weights[static_cast<int64_t>(t) * p.top_k + k] = prob;
         atomicAdd(&hist[e], 1);
       }
+    }
+    if constexpr (QX) {
+      const int chunks = p.H >> 3;
+#pragma unroll
+      for (int i = 0; i < kQxChunks; ++i)
+        if (e + 64 * i >= chunks) xr[i] = i32x4{0, 0, 0, 0};
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kQxChunks; ++i) {
+        float v[8];
+        decode_chunk<QG_BF16>(xr[i], v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+      }
+      amax = wave_max(amax);
+      const float step = fmaxf(amax / 127.0f, 1.0e-20f);
+      const float rstep = __builtin_amdgcn_rcpf(step);
+      int8_t* qr = p.xq + static_cast<int64_t>(t) * p.xq_sm;
+#pragma unroll
+      for (int i = 0; i < kQxChunks; ++i) {
+        const int c = e + 64 * i;
+        quant_chunk_store<QG_BF16, QG_ROUND_HALF_EVEN>(xr[i], step, rstep, qr, c, c < chunks);
+      }
+      if (e == 0) p.xs[t] = step;
     }
   }
   __syncthreads();
@@ -303,7 +349,13 @@ __global__ __launch_bounds__(256) void k_moe_combine(const uint16_t* y, int T, i
 hipError_t launch_moe_dispatch(const MoeDispatchArgs& p, hipStream_t stream) {
   if (p.E > 64) return hipErrorInvalidValue;
   const int nb = p.T > 0 ? ceil_div(p.T, sort_block_tokens(p.T)) : 0;  // <= kMaxSortBlocks
-  if (nb > 0) hipLaunchKernelGGL(k_moe_route, dim3(static_cast<unsigned>(nb)), dim3(kRouteWaves * 64), 0, stream, p);
+  if (p.x != nullptr && (p.H % 8 != 0 || p.H > kMoeRouteQuantMaxH)) return hipErrorInvalidValue;
+  if (nb > 0) {
+    if (p.x != nullptr)
+      hipLaunchKernelGGL(k_moe_route<true>, dim3(static_cast<unsigned>(nb)), dim3(kRouteWaves * 64), 0, stream, p);
+    else
+      hipLaunchKernelGGL(k_moe_route<false>, dim3(static_cast<unsigned>(nb)), dim3(kRouteWaves * 64), 0, stream, p);
+  }
   // one workgroup when there are no tokens: it still writes the empty plan
   hipLaunchKernelGGL(k_moe_scatter, dim3(static_cast<unsigned>(nb > 0 ? nb : 1)), dim3(256), 0, stream, p);
   return hipGetLastError();

@@ -73,7 +73,19 @@ struct MoeDispatchArgs {
   int* tiles;         // [tiles_max][4]
   int tiles_max;
   int tile_rows;
+  // optional (x != nullptr): the routing kernel also quantizes each token's
+  // row of x (bf16 [T, H], row stride x_sm elements) to xq (int8, row stride
+  // xq_sm) and xs (fp32 step per token), half even; H % 8 == 0, H <= 2048
+  const uint16_t* x;
+  int64_t x_sm;
+  int H;
+  int8_t* xq;
+  int64_t xq_sm;
+  float* xs;
 };
+// Largest hidden size whose rows the routing kernel quantizes (one wave per
+// token, 4 chunks of 8 bf16 per lane).
+constexpr int kMoeRouteQuantMaxH = 2048;
 hipError_t launch_moe_dispatch(const MoeDispatchArgs& p, hipStream_t stream);
 // out[t, n] = bf16(sum over k of y[t * top_k + k, n]) (fp32 sum in k order)
 hipError_t launch_moe_combine(const uint16_t* y, int T, int top_k, int H, uint16_t* out, int64_t out_sm,

@@ -77,6 +77,8 @@ SIGNATURES = {
                           _p, _sz, _p]),
     "qg_moe_sizes": (_i, [_i64, _i, _i, _i, _p, _p]),
     "qg_moe_dispatch": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p]),
+    "qg_moe_dispatch_qx": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64,
+                                _i64, _p, _i64, _p, _p]),
     "qg_moe_grouped_gemm": (_i, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _i, _p, _i64, _p, _p,
                                  _p, _p, _i, _p, _i64, _i64, _p]),
     "qg_moe_combine": (_i, [_p, _i64, _i, _i64, _p, _i64, _p]),

@@ -12,7 +12,8 @@ kernels behind the C ABI of include/qgemm.h (qg_moe_*):
 
   dispatch   routing (softmax, top-k by logit), per-expert counting sort with
              segments padded to ``pad`` rows, and the grouped GEMM tile table,
-             all on the GPU (no host synchronisation)
+             all on the GPU (no host synchronisation); for hidden <= 2048 the
+             routing launch also quantizes x per token
   gate/up    grouped GEMM gathering each routed row's token, SiLU * mul
              epilogue -> h bf16 [rows, F]
   quantize   h per routed row (absmax / 127, half even)
@@ -27,6 +28,11 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
+
+
+# Largest hidden size whose x rows the routing launch quantizes itself
+# (include/qgemm.h, qg_moe_dispatch_qx); wider rows take qg_quant_rows_i8.
+MOE_ROUTE_QUANT_MAX_H = 2048
 
 
 @dataclass
@@ -152,12 +158,18 @@ def moe_int8_forward(x: torch.Tensor, router_logits: torch.Tensor, weights: MoeI
     tiles = torch.empty(tiles_n, 4, **i32)
     stream = _lib.stream_of(x)
     P = _lib.ptr
-    _lib.check(lib.qg_moe_dispatch(P(logits), e, t, e, top_k, pad, P(experts), P(rweights), P(counts),
-                                   P(row_token), P(row_weight), P(row_slot), rows, P(tiles), tiles_n, stream),
-               "qg_moe_dispatch")
     xq = torch.empty(t, h, dtype=torch.int8, device=dev)
     xs = torch.empty(t, dtype=torch.float32, device=dev)
-    _quant_rows(x, xq, xs)
+    if h % 8 == 0 and h <= MOE_ROUTE_QUANT_MAX_H and x.data_ptr() % 16 == 0:
+        # the routing launch quantizes x as well (bit-identical to qg_quant_rows_i8)
+        _lib.check(lib.qg_moe_dispatch_qx(P(logits), e, t, e, top_k, pad, P(experts), P(rweights), P(counts),
+                                          P(row_token), P(row_weight), P(row_slot), rows, P(tiles), tiles_n,
+                                          P(x), h, h, P(xq), h, P(xs), stream), "qg_moe_dispatch_qx")
+    else:
+        _lib.check(lib.qg_moe_dispatch(P(logits), e, t, e, top_k, pad, P(experts), P(rweights), P(counts),
+                                       P(row_token), P(row_weight), P(row_slot), rows, P(tiles), tiles_n, stream),
+                   "qg_moe_dispatch")
+        _quant_rows(x, xq, xs)
     hbuf = torch.empty(rows, f, dtype=torch.bfloat16, device=dev)
     _lib.check(lib.qg_moe_grouped_gemm(P(xq), h, t, P(row_token), rows, h, P(weights.w13), h, 2 * f * h, 2 * f, e,
                                        P(tiles), tiles_n, P(xs), P(weights.s13), None, None, _lib.MOE_EPI_SILU_MUL,

@@ -192,3 +192,29 @@ def test_w4a16_workspace_sizes(lib):
     assert lib.qg_w4a16_gemm_workspace_bytes(1024, 4096, 512, 64, 0) == 2 * 4096 * 512  # 88 tiles >= 64
     assert lib.qg_w4a16_gemm_workspace_bytes(1024, 4096, 512, 128, zp) == 0             # 88 tiles < 192
     assert lib.qg_w4a16_gemm_workspace_bytes(64, 200, 512, 32, 0) == 0                  # decode rows
+
+
+def test_moe_dispatch_qx_rejects_invalid_arguments(lib):
+    """The fused routing + x quantization takes bf16 rows of at most 2048
+    values, a multiple of 8, 16-byte aligned x and 8-byte aligned xq rows;
+    anything else is refused before any HIP call (the caller then runs the
+    dispatch and the quantizer separately)."""
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    rows, tiles = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.qg_moe_sizes(16, 8, 2, 64, ctypes.byref(rows), ctypes.byref(tiles)) == 0
+    base = dict(logits=p, l_sm=8, tokens=16, e=8, top_k=2, pad=64, experts=p, weights=p, counts=p, row_token=p,
+                row_weight=p, row_slot=p, rows_max=rows.value, tiles=p, tiles_max=tiles.value, x=p, x_sm=256,
+                hidden=256, xq=p, xq_sm=256, xs=p, stream=None)
+
+    def call(**kw):
+        args = dict(base, **kw)
+        return lib.qg_moe_dispatch_qx(*args.values())
+
+    assert call(hidden=2056, x_sm=2056, xq_sm=2056) == INVALID  # wider than one wave's row
+    assert call(hidden=252, x_sm=252, xq_sm=252) == INVALID     # not a multiple of 8
+    assert call(x_sm=255) == INVALID                            # x_sm < hidden
+    assert call(x_sm=260) == INVALID                            # rows not 16-byte aligned
+    assert call(x=ctypes.c_void_p(4104)) == INVALID             # x not 16-byte aligned
+    assert call(xq=ctypes.c_void_p(4100)) == INVALID            # xq not 8-byte aligned
+    assert call(xs=None) == INVALID
+    assert call(rows_max=0) == INVALID                          # the dispatch's own checks come first

@@ -132,7 +132,7 @@ def run_and_check(cuda, x, logits, wg, wu, wd, top_k, sample=None, label=""):
 
 
 @pytest.mark.parametrize("t,e,h,f,top_k", [(96, 8, 256, 128, 2), (300, 16, 512, 256, 4), (64, 64, 256, 128, 8),
-                                           (1, 4, 128, 128, 1)])
+                                           (1, 4, 128, 128, 1), (40, 8, 2560, 128, 2)])
 def test_moe_small(cuda, t, e, h, f, top_k):
     case(f"moe small t{t} e{e} h{h} f{f} k{top_k}")
     x, logits, wg, wu, wd = make_case(t + e, t, e, h, f, top_k)

@@ -111,6 +111,7 @@ def build(hipcc=None, jobs=None, verbose=False):
     record = {
         "compile_flags": COMMON_FLAGS, "target": ARCH, "compiler_version": version,
         "sources": {s.name: hashlib.sha256(s.read_bytes()).hexdigest() for s in srcs},
+        "internal_headers": {h.name: hashlib.sha256(h.read_bytes()).hexdigest() for h in sorted(CSRC.glob("*.h"))},
         "header_sha256": hashlib.sha256((INCLUDE / "qgemm.h").read_bytes()).hexdigest(),
         "seconds": time.perf_counter() - t0, "returncode": int(failed),
     }

@@ -773,7 +773,7 @@ __device__ __forceinline__ f32x4 col4(const float* v, int c0) { return *reinterp
 // Full tiles are staged per wave in its own part of the rings and leave as
 // whole 16-byte row chunks; edge tiles store element-wise.
 template <typename G, int OUT, int MODE, bool RES, int STAGE_BASE = 0, int REGION = G::RING / G::NW,
-          typename ACCV = i32x16>
+          bool NT = false, typename ACCV = i32x16>
 __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&acc)[G::FM][G::FN], char* smem,
                                             int m0, int n0, int wr, int wc, int wave, int lane) {
 #pragma clang fp contract(off)
@@ -860,7 +860,13 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
         const i32x4 v = *reinterpret_cast<const i32x4*>(region + rr * ROWB + cc * 16);
         const int64_t grow = m0 + wr * G::WM + decltype(pass)::value * PF * 32 + rr;
         const int64_t gcol = n0 + wc * G::WN;
-        *reinterpret_cast<i32x4*>(out + (grow * ldo + gcol) * ES + cc * 16) = v;
+        i32x4* dst = reinterpret_cast<i32x4*>(out + (grow * ldo + gcol) * ES + cc * 16);
+        // NT (the INT8 kernel): non-temporal stores, measured on one box in
+        // alternating runs: cfg1 chain 1962-1975 -> 2014-2024 TOPS, cfg0
+        // 37.2-37.5 -> 36.5-37.2 us; the 2-byte kernels keep plain stores
+        // (FP8 cfg3 and the W4A16 prefill measured the same or 1 % slower)
+        if constexpr (NT) __builtin_nontemporal_store(v, dst);
+        else *dst = v;
       }
     });
   } else {
@@ -992,7 +998,7 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     // tile's stage-0 copies
     stores_fly = PREF && m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((out_ld(p) * out_size<OUT>()) % 16) == 0 &&
                  (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
-    pp_epilogue<G, OUT, MODE, RES, EPI_BASE, EPI_REGION>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
+    pp_epilogue<G, OUT, MODE, RES, EPI_BASE, EPI_REGION, ES == 1>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
     if (!more) break;
     wait_lds_barrier();
     t = tn;

@@ -196,7 +196,6 @@ template <typename T>
 __device__ __forceinline__ T load_at(const void* base, uint32_t byte_off) {
   return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off);
 }
-
 template <int FM, int CT, int G, bool KN, bool F16A, int DEPTH, int WAVES, bool UINT4>
 __global__ __launch_bounds__(64 * WAVES) void k_w4_skinny(W4Args p) {
 #pragma clang fp contract(off)
@@ -806,8 +805,9 @@ hipError_t launch_skinny_t(const W4Args& p, hipStream_t stream) {
 //                (0 2 4 6 1 3 5 7) per 8 for the 7-op nibble unpack;
 //   scales       8 B per column (groups 4 w .. 4 w + 3), one 4-byte copy per lane;
 //   zero points  the packed word holding those groups, lanes 0-31;
-//   weights      8 copies of 4 columns x 256 B (two whole cache lines per
-//                column): copy i, lane L lands in 16-byte slot 64 i + L =
+//   weights      8 non-temporal copies (each byte is read once per call) of
+//                4 columns x 256 B (two whole cache lines per column): copy
+//                i, lane L lands in 16-byte slot 64 i + L =
 //                c * 16 + (k ^ (c & 14)), c = 4 i + L / 16 the local column and
 //                k the 16-byte chunk of its 256 B. The XOR makes the MFMA-layout
 //                reads below (lane (col, q) -> chunk 4 g + q of column col)
@@ -848,7 +848,7 @@ __global__ __launch_bounds__(512) void k_w4_gemv1(W4Args p) {
       const int c = 4 * i + (lane >> 4);
       const int k = (lane & 15) ^ (c & 14);
       const int n = min(n0 + c, p.N - 1);
-      dma16s(p.w, 4u * (static_cast<uint32_t>(n) * KW + 64 * wave + 4 * k), lds_addr_of(wt + 1024 * i));
+      dma16s_nt(p.w, 4u * (static_cast<uint32_t>(n) * KW + 64 * wave + 4 * k), lds_addr_of(wt + 1024 * i));
     });
     wait_vm<8>();  // activations, scales, zero points (the 8 weight copies may fly)
     {
@@ -1023,13 +1023,14 @@ hipError_t launch_w4_unpack(const W4Args& p, hipStream_t stream) {
 
 // Plain read floor: the bytes are split evenly over the waves of a grid of
 // four 512-thread workgroups per CU; each wave reads its contiguous share as
-// whole 1 KB requests (16 bytes per lane), 4 issued back to back per round,
+// whole 1 KB non-temporal requests (16 bytes per lane; 6.03 against 6.31-6.34
+// us without the hint for the cfg2 weight bytes), 4 issued back to back per round,
 // folds them into one word and stores it only if it equals a constant (so the
 // loads stay live). Of the shapes measured for a 30.5 MB read on MI355X (256
 // to 4096 workgroups of 4 to 16 waves, 4 to 16 requests per round, register
-// loads and direct-to-LDS copies), this one and its neighbours are the
-// fastest (6.2-6.3 us); two workgroups per CU with 8 requests per round, the
-// shape of the W4A16 decode, took 6.8 us.
+// loads and direct-to-LDS copies, all without the hint), this one and its
+// neighbours were the fastest (6.2-6.3 us); two workgroups per CU with 8
+// requests per round, the shape of the W4A16 decode, took 6.8 us.
 __global__ __launch_bounds__(512) void k_read_floor(const char* src, uint64_t bytes, uint64_t share,
                                                     uint32_t* sink) {
   constexpr int LPW = 4;
@@ -1042,7 +1043,7 @@ __global__ __launch_bounds__(512) void k_read_floor(const char* src, uint64_t by
     i32x4 v[LPW];
     static_for<0, LPW>([&](auto i) {
       const uint64_t off = o + 1024u * decltype(i)::value + 16u * lane;
-      v[i] = off < end ? *reinterpret_cast<const i32x4*>(src + off) : i32x4{0, 0, 0, 0};
+      v[i] = off < end ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(src + off)) : i32x4{0, 0, 0, 0};
     });
     static_for<0, LPW>([&](auto i) { x ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3]; });
   }

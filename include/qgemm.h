@@ -433,8 +433,9 @@ int qg_moe_combine(const void* y, int64_t tokens, int top_k, int64_t hidden, voi
 /* ---------------------------------------------------------------------------
  * Plain HBM read (a measurement aid; no counterpart in the reference): reads
  * `bytes` bytes at src (16-byte aligned, bytes a multiple of 16) once, split
- * evenly over four 512-thread workgroups per CU, as whole 1 KB wave requests
- * with 4 in flight per wave, and folds them into one word; sink (one uint32)
+ * evenly over four 512-thread workgroups per CU, as whole 1 KB non-temporal
+ * wave requests with 4 in flight per wave (the W4A16 decode streams its
+ * weights with the same hint), and folds them into one word; sink (one uint32)
  * is written only if that word equals a fixed constant. Its time is the floor
  * a weight-streaming kernel such as the W4A16 decode is measured against.
  * ------------------------------------------------------------------------- */

@@ -25,7 +25,8 @@ its ``read_floor`` is qg_read_floor over the same byte count, rotated the same
 way (the plain-read floor of this box).
 ``roofline_cfg0`` is the INT8 GEMM alone at BASELINE configuration 0, where
 the metric's >= 60 % bar is quoted. ``secondary`` holds cfg0's quantizer,
-W4A16 M = 16 / 2048, the FP8 configuration 3, MoE (configuration 4) and W4A8.
+W4A16 M = 16 / 2048, the FP8 configuration 3, MoE (configuration 4), W4A8
+and the MOSS production INT8 shapes (M 1061, fp32 out).
 
 Timing protocol (the reference's, rdna2-ops/bench_int8_gemm.py:259-268):
 --rounds alternating rounds (forward order on even rounds, reverse on odd) of
@@ -69,7 +70,7 @@ def parse():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--rounds", type=int, default=3,
                     help="alternating timing rounds; every figure is the median over rounds")
-    ap.add_argument("--only", choices=("w4a16", "fp8", "moe", "w4a8", "cfg0", "decode"), default=None,
+    ap.add_argument("--only", choices=("w4a16", "fp8", "moe", "w4a8", "cfg0", "decode", "moss"), default=None,
                     help="run one secondary measurement alone and print it (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -504,6 +505,80 @@ def run_w4a8(torch, dev, iters=20):
     return res
 
 
+# The reference's fused INT8 GEMM on the four MOSS production shapes (M 1061,
+# fp32 out, rounding="separate", no bias, weight.T view) on its gfx1030 box, ms
+# (rdna2-ops/results/int8_gemm_moss_shapes_v05.json rows 0-3,
+# RDNA2_OPTIMIZATION_GUIDE_KO.md:1135-1138): context only, other hardware.
+MOSS_SHAPES = ((3072, 3072, 0.698), (9216, 3072, 1.869), (16384, 3072, 3.302), (3072, 8192, 1.932))
+
+
+def run_moss(torch, lib, _lib, dev, iters=50):
+    """Secondary: the MOSS INT8 production calls (M = 1061 tokens; (N, K) of
+    the four projections), the shapes the reference's own INT8 numbers are
+    quoted on. Per shape:
+      kernel  — qg_int8_gemm on preallocated buffers (int8 rows, the weight.T
+                view, fp32 out, order F without bias = the reference's
+                rounding="separate" contract), HIP-graph replays of 50 launches;
+      int8_gemm_dequant — the Python operator as MOSS calls it (fresh output,
+                validation, ctypes), back-to-back calls timed with events;
+      comfy_eager — the product step of comfy_int8.int8_linear's intercepted
+                fp32 path: int8_gemm_dequant with epilogue_order="eager" (the
+                same launch: orders F and E coincide for fp32 output);
+      w8a8_linear — this library's quantizer + GEMM on fp32 x (qg_w8a8_linear).
+    TOPS = 2 M N K per call."""
+    from rdna2_ops.int8_gemm import int8_gemm_dequant, w8a8_linear
+    from rdna2_ops.quantize import quantize_int8_rowwise
+    m = 1061
+    gen = torch.Generator().manual_seed(11)
+    res = {}
+    s = torch.cuda.current_stream(dev)
+
+    def events(fn):
+        samples = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(iters):
+                fn()
+            e1.record(s)
+            e1.synchronize()
+            samples.append(e0.elapsed_time(e1) / iters)
+        return statistics.median(samples)
+
+    for n, k, ref_ms in MOSS_SHAPES:
+        x = torch.randn(m, k, generator=gen).to(dev)
+        wq, ws = quantize_int8_rowwise((torch.randn(n, k, generator=gen) * 0.02).to(dev))
+        ws = ws.reshape(-1).contiguous()
+        xq, xs = quantize_int8_rowwise(x)
+        xs = xs.reshape(-1).contiguous()
+        out = torch.empty((m, n), dtype=torch.float32, device=dev)
+        P = _lib.ptr
+
+        def kernel(i, stream):
+            _lib.check(lib.qg_int8_gemm(P(xq), k, 1, P(wq), 1, k, m, n, k, P(xs), P(ws), n, None, 0, P(out),
+                                        _lib.F32, 0, None, 0, stream), "moss gemm")
+
+        k_ms = statistics.median(_graph_time(torch, kernel, iters) for _ in range(3))
+        rhs = wq.T
+        api = lambda: int8_gemm_dequant(xq, rhs, xs, ws, None, rounding="separate")
+        eager = lambda: int8_gemm_dequant(xq, rhs, xs, ws, None, out_dtype=torch.float32, epilogue_order="eager")
+        lin = lambda: w8a8_linear(x, wq, ws, out_dtype=torch.float32)
+        for f in (api, eager, lin):
+            f()
+        torch.cuda.synchronize()
+        api_ms, eager_ms, lin_ms = events(api), events(eager), events(lin)
+        ops = 2.0 * m * n * k
+        tops = ops / (k_ms * 1e-3) / 1e12
+        res[f"{m}x{n}x{k}"] = {
+            "kernel_us": round(k_ms * 1e3, 2), "kernel_tops": round(tops, 1),
+            "kernel_frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4),
+            "int8_gemm_dequant_us": round(api_ms * 1e3, 2), "comfy_eager_product_us": round(eager_ms * 1e3, 2),
+            "w8a8_linear_us": round(lin_ms * 1e3, 2),
+            "w8a8_linear_tops": round(ops / (lin_ms * 1e-3) / 1e12, 1),
+            "reference_gfx1030_ms": ref_ms}
+    return res
+
+
 def traffic_record(name):
     """HBM bytes per launch of a kernel, from rocprofv3 --pmc FETCH_SIZE /
     WRITE_SIZE runs (each scaled by the same counter's reading for a plain copy
@@ -636,7 +711,8 @@ def main():
         runs = {"w4a16": lambda: run_w4a16(torch, lib, _lib, dev), "fp8": lambda: run_fp8(torch, lib, _lib, dev),
                 "moe": lambda: run_moe(torch, dev), "w4a8": lambda: run_w4a8(torch, dev),
                 "cfg0": lambda: Cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev).profile_run(),
-                "decode": lambda: run_w4a16(torch, lib, _lib, dev, rows=(1,))}
+                "decode": lambda: run_w4a16(torch, lib, _lib, dev, rows=(1,)),
+                "moss": lambda: run_moss(torch, lib, _lib, dev)}
         res = runs[args.only]()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return
@@ -767,6 +843,7 @@ def main():
         sec["fp8_cfg3"] = run_fp8(torch, lib, _lib, dev)
         sec["moe_cfg4"] = run_moe(torch, dev)
         sec["w4a8"] = run_w4a8(torch, dev)
+        sec["moss_int8"] = run_moss(torch, lib, _lib, dev)
         line["secondary"] = sec
     if not args.no_cpu_baseline:
         from oracle.cpu_baseline import cpu_model, time_cfg1_chain

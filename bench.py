@@ -70,7 +70,9 @@ def parse():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--rounds", type=int, default=3,
                     help="alternating timing rounds; every figure is the median over rounds")
-    ap.add_argument("--only", choices=("w4a16", "fp8", "moe", "w4a8", "cfg0", "decode", "moss"), default=None,
+    ap.add_argument("--only", choices=("w4a16", "fp8", "moe", "w4a8", "cfg0", "decode", "moss", "clock",
+                                       "stages"),
+                    default=None,
                     help="run one secondary measurement alone and print it (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -579,6 +581,101 @@ def run_moss(torch, lib, _lib, dev, iters=50):
     return res
 
 
+def run_clock(torch, lib, _lib, dev, ms_target=20.0):
+    """The shader clock an int8 MFMA load sustains on this board (qg_mfma_clock):
+    every CU runs 8 waves issuing v_mfma_i32_32x32x32_i8 back to back for about
+    ``ms_target`` ms, in three modes (constant operands; random operands; random
+    operands plus the INT8 GEMM's LDS fragment reads). Per mode: the median over
+    waves of shader-clock cycles / 100 MHz ticks (MHz), the SIMD's MFMA issue
+    interval, and the int8 throughput that rate gives at that clock."""
+    res = {}
+    out = torch.zeros(256 * 8 * 2, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream(dev)
+    for mode, label in ((0, "constant_operands"), (1, "random_operands"), (2, "random_operands_gemm_lds_reads")):
+        iters = 20000
+        for _ in range(2):  # warm-up launch, then one sized to ms_target
+            _lib.check(lib.qg_mfma_clock(mode, iters, _lib.ptr(out), s.cuda_stream), "qg_mfma_clock")
+            torch.cuda.synchronize()
+            o = out.cpu().numpy().view("uint32").reshape(-1, 2).astype("float64")
+            us = float(statistics.median(o[:, 1])) / 100.0
+            iters = max(1000, min(1 << 22, int(iters * ms_target * 1e3 / max(us, 1.0))))
+        mhz = statistics.median((o[:, 0] / o[:, 1] * 100.0).tolist())
+        # two waves per SIMD share the pipe: per-SIMD interval = the longer
+        # wave's cycles / all MFMAs the SIMD issued
+        cyc = float(o[:, 0].max())
+        per_mfma_simd = cyc / (iters * 6 * 2)
+        tops = 256 * 4 * 65536.0 / per_mfma_simd * mhz * 1e6 / 1e12
+        res[label] = {"mhz": round(mhz, 1), "cycles_per_mfma_per_simd": round(per_mfma_simd, 2),
+                      "iters": iters, "wave_us_median": round(float(statistics.median(o[:, 1])) / 100.0, 1),
+                      "int8_tops_at_that_rate": round(tops, 1),
+                      "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4)}
+    return res
+
+
+def run_stages(torch, lib, _lib, dev, launches=20):
+    """Where the cycles of the INT8 GEMM go (qg_int8_gemm_stages: the ping-pong
+    kernel with shader-clock stamps), at configuration 0 and the three chain
+    shapes. Per shape, medians over waves (and stages) of the last of
+    ``launches`` back-to-back launches, in shader-clock cycles: the wave's
+    life, the prologue (entry to the first stage), the main loop, the epilogue
+    (to its stores' completion), the stage, and the stage's phases per wave
+    group; the clock (cycles / 100 MHz ticks) and the MFMA-busy fraction of a
+    SIMD over the wave's life (48 MFMAs per stage and SIMD, 32 cycles each)."""
+    import numpy as np
+    res = {}
+    gen = torch.Generator().manual_seed(5)
+    shapes = {"cfg0": (4096, 3072, 3072), "qkv": (4096, 9216, 3072), "down": (4096, 3072, 12288)}
+    s = torch.cuda.current_stream(dev)
+    P = _lib.ptr
+    for name, (m, n, k) in shapes.items():
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=gen).to(dev)
+        w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=gen).to(dev)
+        sa = (torch.rand(m, generator=gen) * 0.01 + 1e-3).to(dev)
+        sw = (torch.rand(n, generator=gen) * 0.01 + 1e-3).to(dev)
+        bias = (torch.randn(n, generator=gen) * 0.01).half().to(dev)
+        out = torch.empty((m, n), dtype=torch.float16, device=dev)
+        grid = min(256, -(-m // 256) * -(-n // 192))
+        words = grid * 8 * 272
+        st = torch.zeros(words, dtype=torch.int32, device=dev)
+        for _ in range(launches):
+            _lib.check(lib.qg_int8_gemm_stages(P(a), P(w), m, n, k, P(sa), P(sw), P(bias), P(out), P(st), words,
+                                               s.cuda_stream), "qg_int8_gemm_stages")
+        torch.cuda.synchronize()
+        raw = st.cpu().numpy().view(np.uint32).reshape(grid, 8, 272).astype(np.int64)
+        S = int(raw[0, 0, 263])
+        ext = raw[:, :, 256:]
+        life = (ext[:, :, 3] - ext[:, :, 0]) % 2 ** 32
+        ticks = (ext[:, :, 5] - ext[:, :, 4]) % 2 ** 32
+        pts = raw[:, :, :256].reshape(grid, 8, 4, 64)
+        X, Y = pts[:, :4], pts[:, 4:]
+        Sx = min(S, 64)
+
+        def med(v):
+            return int(np.median(np.asarray(v) % 2 ** 32))
+        r = {"shape": [m, n, k], "stages": S, "tiles_per_workgroup": -(-(-(-m // 256) * -(-n // 192)) // grid),
+             "mhz": round(float(np.median(life / ticks * 100.0)), 1),
+             "wave_cycles": med(life),
+             # entry to the first stage (one tile per workgroup and at most 64
+             # stages: otherwise stage 0's stamp belongs to a later tile / stage)
+             "prologue": (med(X[:, :, 1, 0] - ext[:, :4, 0])
+                          if S <= 64 and -(-m // 256) * -(-n // 192) <= grid else None),
+             "epilogue": med(ext[:, :, 2] - ext[:, :, 1]),
+             "stage": med(X[:, :, 1, 2:Sx] - X[:, :, 1, 1:Sx - 1]),
+             "mfma_ideal_stage": 48 * 32,
+             "X_mfma_issue": med(X[:, :, 2, 1:Sx - 1] - X[:, :, 1, 1:Sx - 1]),
+             "X_wait_B1": med(X[:, :, 3, 1:Sx - 1] - X[:, :, 2, 1:Sx - 1]),
+             "X_lds_reads_and_copies": med(X[:, :, 0, 2:Sx] - X[:, :, 3, 1:Sx - 1]),
+             "X_wait_B0": med(X[:, :, 1, 1:Sx - 1] - X[:, :, 0, 1:Sx - 1]),
+             "Y_lds_reads_and_copies": med(Y[:, :, 1, 1:Sx - 1] - Y[:, :, 0, 1:Sx - 1]),
+             "Y_wait_copies_B1": med(Y[:, :, 2, 1:Sx - 1] - Y[:, :, 1, 1:Sx - 1]),
+             "Y_mfma_issue": med(Y[:, :, 3, 1:Sx - 1] - Y[:, :, 2, 1:Sx - 1]),
+             "Y_to_B0": med(Y[:, :, 0, 2:Sx] - Y[:, :, 3, 1:Sx - 1])}
+        tiles = -(-m // 256) * -(-n // 192)
+        r["mfma_busy_of_wave_life"] = round(48 * 32 * S * tiles / grid / r["wave_cycles"], 4)
+        res[name] = r
+    return res
+
+
 def traffic_record(name):
     """HBM bytes per launch of a kernel, from rocprofv3 --pmc FETCH_SIZE /
     WRITE_SIZE runs (each scaled by the same counter's reading for a plain copy
@@ -712,7 +809,9 @@ def main():
                 "moe": lambda: run_moe(torch, dev), "w4a8": lambda: run_w4a8(torch, dev),
                 "cfg0": lambda: Cfg0(torch, lib, _lib, quantize_int8_rowwise, synthetic, dev).profile_run(),
                 "decode": lambda: run_w4a16(torch, lib, _lib, dev, rows=(1,)),
-                "moss": lambda: run_moss(torch, lib, _lib, dev)}
+                "moss": lambda: run_moss(torch, lib, _lib, dev),
+                "clock": lambda: run_clock(torch, lib, _lib, dev),
+                "stages": lambda: run_stages(torch, lib, _lib, dev)}
         res = runs[args.only]()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return

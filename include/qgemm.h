@@ -441,6 +441,40 @@ int qg_moe_combine(const void* y, int64_t tokens, int top_k, int64_t hidden, voi
  * ------------------------------------------------------------------------- */
 int qg_read_floor(const void* src, size_t bytes, uint32_t* sink, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * MFMA clock probe (a measurement aid; no counterpart in the reference): 256
+ * workgroups of 8 waves (two per SIMD) each issue `iters` (1 .. 2^22) rounds of
+ * six independent v_mfma_i32_32x32x32_i8 back to back; mode 0 keeps the
+ * operands constant, mode 1 cycles them through random fragments, mode 2 adds
+ * the INT8 GEMM's LDS fragment reads (two A and three W 1 KB reads per six
+ * MFMAs). out (uint32 [256 * 8 * 2]): per wave, the shader-clock cycles
+ * (s_memtime) and the 100 MHz real-time ticks (s_memrealtime) of its loop.
+ * Their ratio is the shader clock that MFMA load sustains under the board's
+ * power limit; cycles / (6 * iters) is the issue interval per MFMA of a wave.
+ * ------------------------------------------------------------------------- */
+int qg_mfma_clock(int mode, int iters, uint32_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Stage timing of the INT8 GEMM (a measurement aid; no counterpart in the
+ * reference): the persistent ping-pong kernel that qg_int8_gemm runs for grids
+ * of >= 192 tiles of 256 x 192, with fp16 output and order F (acc * (sa * sw)
+ * + bias), instantiated with shader-clock stamps. Operands canonical: a int8
+ * [m, k] and w int8 [n, k] row-major, 16-byte aligned, k a multiple of 128;
+ * a_scale [m], w_scale [n] fp32; bias_f16 [n] or NULL; out_f16 [m, n].
+ * stamps (uint32, at least min(tiles, 256) * 8 * 272 words): per wave w of
+ * workgroup b, 272 words at (8 b + w) * 272 — words 64 P + s hold point P of
+ * stage s (s < 64) of the last tile the workgroup ran: waves 0-3 before the
+ * stage's first barrier, after it, after their MFMAs, after the second
+ * barrier; waves 4-7 after the first barrier, their LDS reads complete,
+ * after the second barrier, after their MFMAs; then word 256 entry, 257
+ * main-loop exit, 258 epilogue end (its stores complete), 259 exit (shader-
+ * clock cycles), 260 / 261 entry / exit in 100 MHz ticks, 262 the hardware
+ * id, 263 the stage count.
+ * ------------------------------------------------------------------------- */
+int qg_int8_gemm_stages(const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k, const float* a_scale,
+                        const float* w_scale, const void* bias_f16, void* out_f16, uint32_t* stamps,
+                        size_t stamp_words, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -83,6 +83,11 @@ extern "C" int qg_read_floor(const void* src, size_t bytes, uint32_t* sink, void
   return qg::launch_read_floor(src, bytes, sink, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int qg_mfma_clock(int mode, int iters, uint32_t* out, void* stream) {
+  if (mode < 0 || mode > 2 || iters < 1 || iters > (1 << 22) || !out) return hipErrorInvalidValue;
+  return qg::launch_mfma_clock(mode, iters, out, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int qg_quant_rows_i8(const void* x, int x_dtype, int64_t x_sm, int64_t x_sk, int64_t m,
                                 int64_t k, int8_t* q, int64_t q_sm, float* step, int rounding,
                                 void* stream) {
@@ -191,6 +196,35 @@ extern "C" int qg_int8_gemm(const int8_t* a, int64_t a_sm, int64_t a_sk, const i
   return int8_gemm_impl(a, a_sm, a_sk, b, b_sk, b_sn, m, n, k, a_scale, b_scale, b_scale_numel,
                         bias, bias_dtype, out, out_dtype, epilogue, workspace, workspace_bytes,
                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qg_int8_gemm_stages(const int8_t* a, const int8_t* w, int64_t m, int64_t n, int64_t k,
+                                   const float* a_scale, const float* w_scale, const void* bias_f16, void* out_f16,
+                                   uint32_t* stamps, size_t stamp_words, void* stream) {
+  if (m <= 0 || n <= 0 || k <= 0 || k > kMaxK || m > kIntMax || n > kIntMax) return hipErrorInvalidValue;
+  if (!a || !w || !a_scale || !w_scale || !out_f16 || !stamps) return hipErrorInvalidValue;
+  if (!canonical_rows(a, k, 1, m, k) || !canonical_rows(w, k, 1, n, k) || !aligned16(out_f16))
+    return hipErrorInvalidValue;
+  if (m * k >= kMaxOperandBytes || n * k >= kMaxOperandBytes) return hipErrorInvalidValue;
+  const int64_t tiles = ((m + 255) / 256) * ((n + 191) / 192);
+  const int64_t grid = tiles < 256 ? tiles : 256;
+  if (stamp_words < static_cast<size_t>(grid * 8 * qg::kStampWords)) return hipErrorInvalidValue;
+  qg::I8GemmArgs p{};
+  p.a = a;
+  p.a_sm = k;
+  p.w = w;
+  p.w_sn = k;
+  p.M = static_cast<int>(m);
+  p.N = static_cast<int>(n);
+  p.K = static_cast<int>(k);
+  p.a_scale = a_scale;
+  p.b_scale = w_scale;
+  p.bias = bias_f16;
+  p.bias_dtype = QG_F16;
+  p.out = out_f16;
+  p.out_dtype = QG_F16;
+  p.stamps = stamps;
+  return qg::launch_i8_gemm_stages(p, static_cast<hipStream_t>(stream));
 }
 
 namespace {

@@ -597,10 +597,15 @@ constexpr int pp_copies() { return (G::BM > G::BN ? G::BM : G::BN) / 32; }
 // ST > 0: with `pre` and `stores_fly`, the previous tile's epilogue issued at
 // least ST vector stores per wave after the stage-0 copies; the prologue waits
 // let them stay in flight instead of draining every store first.
-template <typename G, typename MF, int ST = 0, typename Park>
+// STAMP (the stage-timing instantiation only): the shader-clock counter is
+// read at four points of every stage, lane s of stv[P] keeping point P of
+// stage s (s < 64): group X before B0, after B0, after its MFMAs, after B1;
+// group Y after B0, its LDS reads complete, after B1, after its MFMAs.
+template <typename G, typename MF, int ST = 0, bool STAMP = false, typename Park>
 __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::FN], char* smem, const char* a_base,
                                             const char* w_base, const uint32_t (&voff)[pp_copies<G>()], int S,
-                                            int wave, int lane, bool pre, Park&& park, bool stores_fly = false) {
+                                            int wave, int lane, bool pre, Park&& park, bool stores_fly = false,
+                                            uint32_t* stv = nullptr) {
   static_assert(G::NW == 8 && G::NA == 3 && G::KT == 4, "ping-pong geometry");
   constexpr bool W8 = G::W8;
   constexpr int KSW = W8 ? G::KS / 2 : G::KS;             // W bytes per row and stage
@@ -682,6 +687,12 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
+  auto stamp = [&](int point, int s) __attribute__((always_inline)) {
+    if constexpr (STAMP) {
+      const uint32_t t = static_cast<uint32_t>(__builtin_amdgcn_s_memtime());
+      stv[point] = lane == (s & 63) ? t : stv[point];
+    }
+  };
 
   if (S <= 0) {
     park();
@@ -700,9 +711,13 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
     if (S > 1) load_phase(T_{}, T_{}, 0, 1);
     else load_phase(T_{}, F_{}, 0, 0);
     for (int s = 0; s < S; ++s) {
+      stamp(0, s);
       __builtin_amdgcn_s_barrier();  // B0(s)
+      stamp(1, s);
       mfma_phase();
+      stamp(2, s);
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1(s)
+      stamp(3, s);
       if (s + 2 < S) load_phase(T_{}, T_{}, s + 1, s + 2);
       else if (s + 1 < S) load_phase(T_{}, F_{}, s + 1, 0);
     }
@@ -721,14 +736,25 @@ __device__ __forceinline__ void pp_mainloop(typename MF::acc_t (&acc)[G::FM][G::
     wait_lds_barrier();
     for (int s = 0; s < S; ++s) {
       __builtin_amdgcn_s_barrier();  // B0(s)
+      stamp(0, s);
       if (s + 2 < S) {
         load_phase(F_{}, T_{}, s, s + 2);
+        if constexpr (STAMP) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          stamp(1, s);
+        }
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(YS) : "memory");  // B1(s)
       } else {
         load_phase(F_{}, F_{}, s, 0);
+        if constexpr (STAMP) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          stamp(1, s);
+        }
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // B1(s)
       }
+      stamp(2, s);
       mfma_phase();
+      stamp(3, s);
     }
   }
 }
@@ -903,7 +929,12 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
 // The body is shared by the INT8 kernel (MF = MfmaI8, 1-byte operands) and the
 // 2-byte kernel (MfmaHalf, fp16 / bf16 operands: a 128-byte stage row holds 64
 // K elements, four 32x32x16 k-steps); ES is the operand element size.
-template <typename G, int OUT, int MODE, typename MF, int ES, bool RES>
+//
+// STAMP (qg_int8_gemm_stages only): each wave also records the main loop's
+// stage stamps (pp_mainloop) and its entry, main-loop exit, epilogue end
+// (after its stores completed) and exit, written to p.stamps at the end; the
+// values of the last tile a workgroup computed are kept.
+template <typename G, int OUT, int MODE, typename MF, int ES, bool RES, bool STAMP = false>
 __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
 #pragma clang fp contract(off)
   constexpr int YS = pp_copies<G>();
@@ -963,6 +994,13 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
   constexpr int kStoresPerWave = (PREF && !RES) ? G::FM * (G::WN * out_size<OUT>() / 16) / 2 : 0;
   static_assert(kStoresPerWave + pp_copies<G>() < 64, "vmcnt range");
   typename MF::acc_t acc[G::FM][G::FN];
+  uint32_t stv[4] = {0, 0, 0, 0};
+  uint32_t t_entry = 0, t_loop = 0, t_epi = 0;
+  uint64_t rt_entry = 0;
+  if constexpr (STAMP) {
+    t_entry = static_cast<uint32_t>(__builtin_amdgcn_s_memtime());
+    rt_entry = __builtin_amdgcn_s_memrealtime();
+  }
   for (;;) {
     // The lane index passes through an opaque copy per tile: lane-derived LDS
     // and global offsets of the main loop and the epilogue are then recomputed
@@ -982,7 +1020,9 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
         }
       }
     };
-    pp_mainloop<G, MF, kStoresPerWave>(acc, smem, a_base, w_base, voff, S, wave, lane_t, pre, park, stores_fly);
+    pp_mainloop<G, MF, kStoresPerWave, STAMP>(acc, smem, a_base, w_base, voff, S, wave, lane_t, pre, park,
+                                              stores_fly, stv);
+    if constexpr (STAMP) t_loop = static_cast<uint32_t>(__builtin_amdgcn_s_memtime());
     const int tn = t + static_cast<int>(gridDim.x);
     const bool more = tn < total;
     int m1 = 0, n1 = 0;
@@ -999,6 +1039,10 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     stores_fly = PREF && m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((out_ld(p) * out_size<OUT>()) % 16) == 0 &&
                  (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
     pp_epilogue<G, OUT, MODE, RES, EPI_BASE, EPI_REGION, ES == 1>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
+    if constexpr (STAMP) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      t_epi = static_cast<uint32_t>(__builtin_amdgcn_s_memtime());
+    }
     if (!more) break;
     wait_lds_barrier();
     t = tn;
@@ -1007,11 +1051,34 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     ep = ep1;
     pre = PREF && S > 0;
   }
+  if constexpr (STAMP) {
+    const uint64_t rt_exit = __builtin_amdgcn_s_memrealtime();
+    const uint32_t t_exit = static_cast<uint32_t>(__builtin_amdgcn_s_memtime());
+    uint32_t* o = p.stamps + (static_cast<size_t>(blockIdx.x) * G::NW + wave) * kStampWords;
+    static_for<0, 4>([&](auto q) { o[decltype(q)::value * 64 + lane] = stv[decltype(q)::value]; });
+    if (lane == 0) {
+      o[256] = t_entry;
+      o[257] = t_loop;
+      o[258] = t_epi;
+      o[259] = t_exit;
+      o[260] = static_cast<uint32_t>(rt_entry);
+      o[261] = static_cast<uint32_t>(rt_exit);
+      o[262] = __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));  // HW_ID (CU, SIMD, SE)
+      o[263] = static_cast<uint32_t>(S);
+    }
+  }
 }
 
 template <typename G, int OUT, int MODE, bool RES>
 __global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp(I8GemmArgs p) {
   pp_gemm_body<G, OUT, MODE, MfmaI8, 1, RES>(p);
+}
+
+// Stage-timing instantiation of the ping-pong INT8 GEMM (fp16 output, order
+// F): the same schedule with shader-clock stamps (qg_int8_gemm_stages).
+template <typename G>
+__global__ __launch_bounds__(G::THREADS, 1) void k_i8_gemm_pp_stages(I8GemmArgs p) {
+  pp_gemm_body<G, QG_F16, EPI_F, MfmaI8, 1, false, true>(p);
 }
 
 // fp16 / bf16 A [M, K] and W [N, K] (K a multiple of 64, 16-byte aligned
@@ -1376,6 +1443,15 @@ hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream) {
     default:
       hipLaunchKernelGGL((k_i8_moe_pp<G, QG_MOE_EPI_ROUTE>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_i8_gemm_stages(const I8GemmArgs& p, hipStream_t stream) {
+  using G = I8Geo<256, 192, 4, 2, 3>;
+  const int tiles = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
+  if (tiles == 0) return hipSuccess;
+  hipLaunchKernelGGL((k_i8_gemm_pp_stages<G>), dim3(tiles < kPersistentCUs ? tiles : kPersistentCUs),
+                     dim3(G::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 

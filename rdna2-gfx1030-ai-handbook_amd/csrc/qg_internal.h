@@ -46,7 +46,17 @@ struct I8GemmArgs {
   int out_rows;   // rows of out (routed rows, or tokens * top_k for the route epilogue)
   int n_experts;
   int moe_epi;
+  // Stage-timing instantiation only (launch_i8_gemm_stages): per wave of
+  // workgroup b, kStampWords words at stamps + (8 b + wave) * kStampWords.
+  uint32_t* stamps;
 };
+
+// Stage timing of the ping-pong INT8 GEMM (qg_int8_gemm_stages): words per
+// wave = 4 stamp points x 64 stages (lane s holds stage s, s < 64) + 16
+// (kernel entry, main-loop exit, epilogue end, exit in shader-clock cycles;
+// entry and exit in 100 MHz ticks; the hardware id; the stage count).
+constexpr int kStampWords = 4 * 64 + 16;
+hipError_t launch_i8_gemm_stages(const I8GemmArgs& p, hipStream_t stream);
 
 hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream);
 hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream);
@@ -55,6 +65,11 @@ hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream);
 hipError_t launch_h16_gemm(const I8GemmArgs& p, bool f16a, hipStream_t stream);
 // Plain streaming read of `bytes` (a multiple of 16) at a 16-byte aligned src.
 hipError_t launch_read_floor(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream);
+// MFMA clock probe (qg_mfma_clock): kMfmaClockWorkgroups workgroups of 8 waves,
+// out[2 * (8 b + w) + {0, 1}] = shader-clock cycles and 100 MHz ticks of wave w
+// of workgroup b.
+constexpr int kMfmaClockWorkgroups = 256;
+hipError_t launch_mfma_clock(int mode, int iters, uint32_t* out, hipStream_t stream);
 // fp16 / bf16 A against fp8 W converted in registers (fp8 W stages in LDS).
 hipError_t launch_f8w_gemm(const I8GemmArgs& p, bool f16a, bool e5, hipStream_t stream);
 

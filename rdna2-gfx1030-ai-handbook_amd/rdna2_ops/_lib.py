@@ -52,6 +52,8 @@ SIGNATURES = {
     "qg_error_string": (ctypes.c_char_p, [_i]),
     "qg_version": (ctypes.c_char_p, []),
     "qg_read_floor": (_i, [_p, _sz, _p, _p]),
+    "qg_mfma_clock": (_i, [_i, _i, _p, _p]),
+    "qg_int8_gemm_stages": (_i, [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _sz, _p]),
     "qg_quant_rows_i8": (_i, [_p, _i, _i64, _i64, _i64, _i64, _p, _i64, _p, _i, _p]),
     "qg_int8_gemm_workspace_bytes": (_sz, [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64]),
     "qg_int8_gemm": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i,

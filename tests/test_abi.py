@@ -96,6 +96,34 @@ def test_read_floor_rejects_invalid_arguments(lib):
     assert lib.qg_read_floor(p, 32, None, None) == INVALID
 
 
+def test_mfma_clock_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(16)
+    assert lib.qg_mfma_clock(3, 10, p, None) == INVALID            # mode
+    assert lib.qg_mfma_clock(-1, 10, p, None) == INVALID
+    assert lib.qg_mfma_clock(1, 0, p, None) == INVALID             # iterations
+    assert lib.qg_mfma_clock(1, (1 << 22) + 1, p, None) == INVALID
+    assert lib.qg_mfma_clock(1, 10, None, None) == INVALID         # output
+
+
+def test_int8_gemm_stages_rejects_invalid_arguments(lib):
+    p = ctypes.c_void_p(256)
+    words = 256 * 8 * 272
+    ok = [p, p, 4096, 3072, 3072, p, p, None, p, p, words, None]
+    bad_k = list(ok)
+    bad_k[4] = 3000                                                # k % 128
+    assert lib.qg_int8_gemm_stages(*bad_k) == INVALID
+    few = list(ok)
+    few[10] = words - 1                                            # stamp buffer too small
+    assert lib.qg_int8_gemm_stages(*few) == INVALID
+    unaligned = list(ok)
+    unaligned[0] = ctypes.c_void_p(264)                            # 16-byte aligned operands
+    assert lib.qg_int8_gemm_stages(*unaligned) == INVALID
+    for i in (0, 1, 5, 6, 8, 9):                                   # required pointers
+        missing = list(ok)
+        missing[i] = None
+        assert lib.qg_int8_gemm_stages(*missing) == INVALID
+
+
 def test_rot_quant_rows_rejects_invalid_arguments(lib):
     p = ctypes.c_void_p(16)
 

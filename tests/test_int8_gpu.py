@@ -382,3 +382,60 @@ def test_int8_random_shape_sweep(cuda, m, n, k):
     got = int8_gemm_dequant(ag, wg.T, sa.to(cuda), sb.to(cuda), bias.to(cuda), out_dtype=torch.bfloat16)
     ref = o.epilogue_f(acc_o, sa.numpy(), sb.numpy(), bias.float().numpy(), out="bf16")
     assert np.array_equal(_bits(got, "bf16"), _bits(ref, "bf16"))
+
+
+def test_mfma_clock_probe_counts_cycles(cuda):
+    """qg_mfma_clock (the MFMA clock probe): every wave reports its loop's
+    shader-clock cycles and 100 MHz ticks; six independent 32x32x32 int8 MFMAs
+    per round issue at no less than the pipe's 32 cycles each per wave, and the
+    clock implied by the two counters lies in the MI355X's range."""
+    from rdna2_ops import _lib
+    lib = _lib.library()
+    for mode in (0, 1, 2):
+        case(f"mfma clock mode {mode}")
+        out = torch.zeros(256 * 8 * 2, dtype=torch.int32, device=cuda)
+        _lib.check(lib.qg_mfma_clock(mode, 2000, _lib.ptr(out), _lib.stream_of(out)), "qg_mfma_clock")
+        torch.cuda.synchronize()
+        o = out.cpu().numpy().view(np.uint32).reshape(-1, 2).astype(np.float64)
+        assert (o[:, 1] > 0).all()
+        per_mfma = o[:, 0] / (6 * 2000)
+        assert (per_mfma >= 31.5).all(), per_mfma.min()
+        mhz = o[:, 0] / o[:, 1] * 100.0
+        assert 300.0 < float(np.median(mhz)) < 2600.0, float(np.median(mhz))
+
+
+def test_int8_gemm_stages_matches_the_gemm(cuda):
+    """qg_int8_gemm_stages (the ping-pong kernel with shader-clock stamps) runs
+    the same schedule as qg_int8_gemm: bit-identical fp16 output on a grid of
+    192 tiles of 256 x 192, stamps in order within every stage."""
+    from rdna2_ops import _lib
+    lib = _lib.library()
+    case("int8 gemm stages 4096x2304x384")
+    m, n, k = 4096, 2304, 384
+    g = torch.Generator().manual_seed(21)
+    a = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8).to(cuda)
+    w = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8).to(cuda)
+    sa = (torch.rand(m, generator=g) * 0.01 + 1e-3).to(cuda)
+    sw = (torch.rand(n, generator=g) * 0.01 + 1e-3).to(cuda)
+    bias = (torch.randn(n, generator=g) * 0.1).half().to(cuda)
+    ref = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    out = torch.empty_like(ref)
+    P, s = _lib.ptr, _lib.stream_of(a)
+    _lib.check(lib.qg_int8_gemm(P(a), k, 1, P(w), 1, k, m, n, k, P(sa), P(sw), n, P(bias), _lib.F16, P(ref),
+                                _lib.F16, 0, None, 0, s), "qg_int8_gemm")
+    words = 192 * 8 * 272
+    st = torch.zeros(words, dtype=torch.int32, device=cuda)
+    _lib.check(lib.qg_int8_gemm_stages(P(a), P(w), m, n, k, P(sa), P(sw), P(bias), P(out), P(st), words, s),
+               "qg_int8_gemm_stages")
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    raw = st.cpu().numpy().view(np.uint32).reshape(192, 8, 272).astype(np.int64)
+    assert (raw[:, :, 263] == k // 128).all()
+    stages = k // 128
+    pts = raw[:, :, :256].reshape(192, 8, 4, 64)[:, :, :, :stages]
+    step = (np.diff(pts, axis=2) % 2 ** 32)
+    assert (step < 2 ** 20).all()  # the four points of a stage come in order
+    ext = raw[:, :, 256:]
+    assert (((ext[:, :, 3] - ext[:, :, 0]) % 2 ** 32) > 0).all()
+    assert (((ext[:, :, 5] - ext[:, :, 4]) % 2 ** 32) > 0).all()
+

@@ -45,7 +45,8 @@ _GROUPS = (32, 64, 128)
 
 @dataclass
 class PackedInt4:
-    """Caller-owned W4 weight (int4_weight_gemm_v07.py:20-46).
+    """Caller-owned W4 weight (int4_weight_gemm_v07.py:20-46; derived from the
+    reference's container, see the notice above pack_int4_cpu).
 
     ``signed`` / ``zeros_packed`` describe the storage coordinates: the
     reference format is signed=True, zeros_packed=False (int32 zero points);
@@ -91,6 +92,34 @@ class PackedInt4:
 
 
 # ------------------------------------------------------------------ CPU packing
+# PackedInt4 above and pack_int4_cpu / unpack_int4_cpu below are derived from
+# rdna2-ops/rdna2_ops/int4_weight_gemm_v07.py:20-92 (the storage container and
+# the CPU pack rule are the interchange format packed weights must share with
+# the reference; the expressions follow the reference's, with an int32-wrap
+# fix and a shared shift helper). That code's notice:
+#
+#   MIT License
+#
+#   Copyright (c) 2026 rdna2-ops contributors
+#
+#   Permission is hereby granted, free of charge, to any person obtaining a
+#   copy of this software and associated documentation files (the
+#   "Software"), to deal in the Software without restriction, including
+#   without limitation the rights to use, copy, modify, merge, publish,
+#   distribute, sublicense, and/or sell copies of the Software, and to permit
+#   persons to whom the Software is furnished to do so, subject to the
+#   following conditions:
+#
+#   The above copyright notice and this permission notice shall be included
+#   in all copies or substantial portions of the Software.
+#
+#   THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS
+#   OR IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF
+#   MERCHANTABILITY, FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN
+#   NO EVENT SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM,
+#   DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR
+#   OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE
+#   USE OR OTHER DEALINGS IN THE SOFTWARE.
 def _shifts(order):
     s = torch.arange(8, dtype=torch.int64) * 4
     return 28 - s if order == "high" else s

@@ -239,6 +239,37 @@ def test_uint4_single_row_kernel(cuda, n, k):
     assert md["variant"] == "w4a16_gemv1" and md["vgpr"] is not None
 
 
+@pytest.mark.parametrize("m", [2, 5, 16])
+@pytest.mark.parametrize("n,k", [(1000, 256), (4100, 1536), (64, 4096), (14336, 4096)])
+def test_uint4_multi_row_decode(cuda, m, n, k):
+    """The 2-16-row decode on the BASELINE storage (bf16 rows, uint4, g128):
+    ragged N, short K (waves past K idle), bias and every output dtype,
+    strided activation rows, against the float64 oracle; the kernel metadata
+    names the decode kernel."""
+    case(f"uint4 multi-row kernel m{m} n{n} k{k}")
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    w = torch.randn(n, k, generator=g) * 0.02
+    a_full = torch.randn(m, k + 24, generator=g).to(torch.bfloat16)
+    b = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16)
+    p = w4().pack_uint4(w.to(cuda), group_size=128)
+    r = o4.pack_uint4_baseline(w.numpy(), group_size=128)
+    cen = o4.dequant_baseline(r, floating=False)
+    s = bf16_bits_to_f32(r["scales"])
+    for strided in (False, True):
+        a = a_full[:, 8:8 + k] if strided else a_full[:, :k].contiguous()
+        av = act_values(a)
+        absmag = o4.w4a16_linear(np.abs(av), np.ones_like(cen), s, 128)
+        ag = a_full.to(cuda)[:, 8:8 + k] if strided else a.to(cuda)
+        for bias in (None, b):
+            y64 = o4.w4a16_linear(av, cen, s, 128, None if bias is None else act_values(bias))
+            for out_dtype in (torch.bfloat16, torch.float16, torch.float32):
+                y = w4().w4a16_gemm(ag, p, None if bias is None else bias.to(cuda), out_dtype=out_dtype)
+                check_product(y, y64, absmag, out_dtype,
+                              f"multi-row m{m} n{n} k{k} strided={strided} bias={bias is not None} {out_dtype}")
+    _, md = w4().int4_linear_a16(a.to(cuda), p, method="dot2", return_kernel=True)
+    assert md["variant"] == "w4a16_decode" and md["vgpr"] is not None
+
+
 def test_decode_metadata_column_tiles(cuda):
     """The decode kernel's reported column tile follows the launcher's choice
     per group size and row count (16 * CT columns)."""

@@ -526,7 +526,11 @@ def run_moss(torch, lib, _lib, dev, iters=50):
       comfy_eager — the product step of comfy_int8.int8_linear's intercepted
                 fp32 path: int8_gemm_dequant with epilogue_order="eager" (the
                 same launch: orders F and E coincide for fp32 output);
-      w8a8_linear — this library's quantizer + GEMM on fp32 x (qg_w8a8_linear).
+      w8a8_linear — this library's quantizer + GEMM on fp32 x (qg_w8a8_linear);
+      w8a8_linear_convrot256_residual — the same with the MOSS linear's
+                opt-in fusions (qg_w8a8_linear_ex): the ConvRot g256 rotation
+                in the quantizer launch and an fp32 residual x per-channel
+                scale in the GEMM epilogue.
     TOPS = 2 M N K per call."""
     from rdna2_ops.int8_gemm import int8_gemm_dequant, w8a8_linear
     from rdna2_ops.quantize import quantize_int8_rowwise
@@ -565,10 +569,16 @@ def run_moss(torch, lib, _lib, dev, iters=50):
         api = lambda: int8_gemm_dequant(xq, rhs, xs, ws, None, rounding="separate")
         eager = lambda: int8_gemm_dequant(xq, rhs, xs, ws, None, out_dtype=torch.float32, epilogue_order="eager")
         lin = lambda: w8a8_linear(x, wq, ws, out_dtype=torch.float32)
-        for f in (api, eager, lin):
+        # the MOSS linear's opt-in fusions (qg_w8a8_linear_ex): ConvRot g256
+        # prologue, fp32 residual with a per-channel scale (4-wave kernel)
+        res_in = torch.randn(m, n, generator=gen).to(dev)
+        res_sc = (torch.rand(n, generator=gen) + 0.5).to(dev)
+        lin_ex = lambda: w8a8_linear(x, wq, ws, out_dtype=torch.float32, convrot_groupsize=256,
+                                     residual=res_in, residual_scale=res_sc)
+        for f in (api, eager, lin, lin_ex):
             f()
         torch.cuda.synchronize()
-        api_ms, eager_ms, lin_ms = events(api), events(eager), events(lin)
+        api_ms, eager_ms, lin_ms, ex_ms = events(api), events(eager), events(lin), events(lin_ex)
         ops = 2.0 * m * n * k
         tops = ops / (k_ms * 1e-3) / 1e12
         res[f"{m}x{n}x{k}"] = {
@@ -577,6 +587,7 @@ def run_moss(torch, lib, _lib, dev, iters=50):
             "int8_gemm_dequant_us": round(api_ms * 1e3, 2), "comfy_eager_product_us": round(eager_ms * 1e3, 2),
             "w8a8_linear_us": round(lin_ms * 1e3, 2),
             "w8a8_linear_tops": round(ops / (lin_ms * 1e-3) / 1e12, 1),
+            "w8a8_linear_convrot256_residual_us": round(ex_ms * 1e3, 2),
             "reference_gfx1030_ms": ref_ms}
     return res
 

@@ -198,6 +198,56 @@ __device__ __forceinline__ uint32_t epi_bits(int32_t acc, float sa, float sb, fl
   }
 }
 
+// The residual value of output element (row, col) in fp32 (p.residual non-null).
+__device__ __forceinline__ float residual_value(const I8GemmArgs& p, int row, int col) {
+  const int64_t idx = static_cast<int64_t>(row) * p.residual_sm + col;
+  if (p.residual_dtype == QG_F32) return static_cast<const float*>(p.residual)[idx];
+  if (p.residual_dtype == QG_F16) return f16_to_f32(static_cast<const uint16_t*>(p.residual)[idx]);
+  return bf16_to_f32(static_cast<const uint16_t*>(p.residual)[idx]);
+}
+
+// The residual values of the 4 adjacent output elements (row, col0 .. col0 + 3)
+// in fp32, one vector load when they lie in the row and are aligned (columns
+// past N read column N - 1: their results are never stored).
+__device__ __forceinline__ f32x4 residual_value4(const I8GemmArgs& p, int row, int col0) {
+  const int64_t idx = static_cast<int64_t>(row) * p.residual_sm + col0;
+  f32x4 r;
+  if (col0 + 3 < p.N && (idx & 3) == 0) {
+    if (p.residual_dtype == QG_F32) return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p.residual) + idx);
+    const uint2 h = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.residual) + idx);
+    const bool f16 = p.residual_dtype == QG_F16;
+    const uint16_t e[4] = {static_cast<uint16_t>(h.x), static_cast<uint16_t>(h.x >> 16), static_cast<uint16_t>(h.y),
+                           static_cast<uint16_t>(h.y >> 16)};
+    static_for<0, 4>([&](auto c) {
+      constexpr int C = decltype(c)::value;
+      r[C] = f16 ? f16_to_f32(e[C]) : bf16_to_f32(e[C]);
+    });
+    return r;
+  }
+  static_for<0, 4>([&](auto c) {
+    constexpr int C = decltype(c)::value;
+    r[C] = residual_value(p, row, min(col0 + C, p.N - 1));
+  });
+  return r;
+}
+
+// The residual scales of output columns col0 .. col0 + 3 (p.residual_scale
+// non-null; columns past N take column N - 1's).
+__device__ __forceinline__ f32x4 residual_scale4(const I8GemmArgs& p, int col0) {
+  if (p.residual_scalar) {
+    const float v = p.residual_scale[0];
+    return f32x4{v, v, v, v};
+  }
+  if (col0 + 3 < p.N && (col0 & 3) == 0 && (reinterpret_cast<uintptr_t>(p.residual_scale) & 15) == 0)
+    return *reinterpret_cast<const f32x4*>(p.residual_scale + col0);
+  f32x4 r;
+  static_for<0, 4>([&](auto c) {
+    constexpr int C = decltype(c)::value;
+    r[C] = p.residual_scale[min(col0 + C, p.N - 1)];
+  });
+  return r;
+}
+
 // The residual term of output element (row, col) (p.residual non-null).
 __device__ __forceinline__ float residual_term(const I8GemmArgs& p, int row, int col) {
 #pragma clang fp contract(off)
@@ -327,12 +377,30 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
   const bool has_bias = p.bias != nullptr;
   const int lh = 4 * (lane >> 5);
   const int lcol = lane & 31;
-  float sb[G::FN], bv[G::FN];
+  float sb[G::FN], bv[G::FN], rs[G::FN];
   static_for<0, G::FN>([&](auto j) {
     const int c = wc * G::WN + j * 32 + lcol;
     sb[j] = MODE != EPI_INT ? sb_lds[c] : 0.0f;
     bv[j] = MODE != EPI_INT ? bias_value(bias_lds[c], p.bias_dtype) : 0.0f;
+    // the residual scale of this lane's column in block j (loaded once)
+    rs[j] = 1.0f;
+    if constexpr (RES) {
+      if (p.residual_scale) rs[j] = p.residual_scale[p.residual_scalar ? 0 : min(n0 + c, p.N - 1)];
+    }
   });
+  const bool has_rs = p.residual_scale != nullptr;
+  // v + residual (x scale): the fp32 order of residual_term
+  auto with_res = [&](float v, int row, int col, float rsc) __attribute__((always_inline)) {
+#pragma clang fp contract(off)
+    float r = residual_value(p, row, col);
+    if (has_rs) r = r * rsc;
+    return v + r;
+  };
+  auto bits_of = [&](float v) __attribute__((always_inline)) -> uint32_t {
+    if constexpr (OUT == QG_F32) return __float_as_uint(v);
+    else if constexpr (OUT == QG_F16) return f32_to_f16(v);
+    else return f32_to_bf16(v);
+  };
   // Scales of the 4 rows 32 i + 8 q + lh + (0..3): one aligned LDS vector.
   auto row_scales = [&](int i, int q) -> f32x4 {
     if constexpr (MODE == EPI_INT) return f32x4{0, 0, 0, 0};
@@ -356,6 +424,20 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
     static_for<0, G::FM / PF>([&](auto pass) {
       static_for<0, PF>([&](auto ii) {
         constexpr int i = decltype(pass)::value * PF + decltype(ii)::value;
+        // the residual values of block row i, all loads issued before any is
+        // used (one memory latency per block row instead of one per element)
+        float rv[RES ? 4 : 1][RES ? G::FN : 1][RES ? 4 : 1];
+        if constexpr (RES) {
+          static_for<0, 4>([&](auto q) {
+            static_for<0, G::FN>([&](auto j) {
+              static_for<0, 4>([&](auto e) {
+                rv[q][j][e] = residual_value(p, m0 + wr * G::WM + 32 * i + 8 * decltype(q)::value + lh +
+                                                    decltype(e)::value,
+                                             n0 + wc * G::WN + decltype(j)::value * 32 + lcol);
+              });
+            });
+          });
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const f32x4 sa = row_scales(i, q);
@@ -363,11 +445,12 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               uint32_t bits;
-              if constexpr (RES)
-                bits = epi_bits_res<OUT, MODE>(p, acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias,
-                                               m0 + wr * G::WM + 32 * i + 8 * q + lh + e,
-                                               n0 + wc * G::WN + j * 32 + lcol);
-              else
+              if constexpr (RES) {
+                // v + f32(residual) (x scale), the fp32 order of residual_term
+                float r = rv[q][j][e];
+                if (has_rs) r = r * rs[j];
+                bits = bits_of(epi_value<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias) + r);
+              } else
                 bits = epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias);
               char* dstp = region + (ii * 32 + 8 * q + lh + e) * ROWB + (j * 32 + lcol) * ES;
               if constexpr (ES == 4) *reinterpret_cast<uint32_t*>(dstp) = bits;
@@ -404,8 +487,9 @@ __device__ __forceinline__ void i8_epilogue(const I8GemmArgs& p, const i32x16 (&
               const int row = row0 + 32 * i + 8 * q + e;
               if (row < p.M)
                 store_elem<OUT>(p.out, static_cast<int64_t>(row) * ldo + col,
-                                RES ? epi_bits_res<OUT, MODE>(p, acc[i][j][4 * q + e], sa[e], sb[j], bv[j],
-                                                              has_bias, row, col)
+                                RES ? bits_of(with_res(epi_value<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j],
+                                                                            bv[j], has_bias),
+                                                       row, col, rs[j]))
                                     : epi_bits<OUT, MODE>(acc[i][j][4 * q + e], sa[e], sb[j], bv[j], has_bias));
             }
           }
@@ -813,6 +897,19 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
   // output bits of the 4 columns of quad g of block (i, j): 4 words (4-byte
   // outputs) or 2 packed words (2-byte outputs) in w[0..]
   // row: the quad's output row; col0: its first output column (residual term)
+  // the residual term (x scale) of the 4 columns col0 .. col0 + 3 of one row
+  auto res_term4 = [&](int row, int col0) __attribute__((always_inline)) -> f32x4 {
+#pragma clang fp contract(off)
+    f32x4 r = residual_value4(p, row, col0);
+    if (p.residual_scale) {
+      const f32x4 rs = residual_scale4(p, col0);
+      static_for<0, 4>([&](auto c) {
+        constexpr int C = decltype(c)::value;
+        r[C] = r[C] * rs[C];
+      });
+    }
+    return r;
+  };
   auto quad_bits = [&](auto i, auto j, auto g, const f32x4& sb4, const f32x4& bv4, uint32_t (&w)[4], int row,
                        int col0) {
     constexpr int r0 = 4 * decltype(g)::value;
@@ -825,9 +922,11 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
         v[C] = epi_value<OUT, MODE>(acc[i][j][r0 + C], sa[i], sb4[C], bv4[C], has_bias);
       });
       if constexpr (RES) {
+        // v + f32(residual) (x scale), the fp32 order of residual_term
+        const f32x4 r = res_term4(row, col0);
         static_for<0, 4>([&](auto c) {
           constexpr int C = decltype(c)::value;
-          v[C] = v[C] + residual_term(p, row, min(col0 + C, p.N - 1));
+          v[C] = v[C] + r[C];
         });
       }
       if constexpr (out_size<OUT>() == 4) {
@@ -1389,11 +1488,9 @@ hipError_t launch_tile(const I8GemmArgs& p, hipStream_t stream) {
   const int blocks = ceil_div(p.M, G::BM) * ceil_div(p.N, G::BN);
   if constexpr (G::NW == 4)
     hipLaunchKernelGGL((k_i8_gemm<G, WPE, OUT, MODE, RES>), dim3(blocks), dim3(G::THREADS), 0, stream, p);
-  else if constexpr (!RES)  // persistent: at most one workgroup per CU (LDS), a multiple of the 8 XCDs
-    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE, false>), dim3(blocks < kPersistentCUs ? blocks : kPersistentCUs),
+  else  // persistent: at most one workgroup per CU (LDS), a multiple of the 8 XCDs
+    hipLaunchKernelGGL((k_i8_gemm_pp<G, OUT, MODE, RES>), dim3(blocks < kPersistentCUs ? blocks : kPersistentCUs),
                        dim3(G::THREADS), 0, stream, p);
-  else
-    return hipErrorInvalidValue;  // launch_i8_gemm sends residual epilogues to the 4-wave kernel
   return hipGetLastError();
 }
 
@@ -1461,8 +1558,7 @@ hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream) {
   // CUs (4096x3072 -> 256 tiles, x9216 -> 768, x12288 -> 1024). Smaller
   // problems use 128x128 tiles so that more CUs get work.
   const long big = static_cast<long>(ceil_div(p.M, 256)) * ceil_div(p.N, 192);
-  // the residual epilogue (an opt-in path) runs on the 4-wave kernel only
-  if (big >= 192 && p.residual == nullptr) return launch_variant<I8Geo<256, 192, 4, 2, 3>, 1>(p, stream);
+  if (big >= 192) return launch_variant<I8Geo<256, 192, 4, 2, 3>, 1>(p, stream);
   return launch_variant<I8Geo<128, 128, 2, 2, 2>, 2>(p, stream);
 }
 

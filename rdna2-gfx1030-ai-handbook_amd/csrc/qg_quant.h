@@ -71,13 +71,12 @@ constexpr float kRiskyDist = 0.5f - 0.0001220703125f;  // 1/2 - 2^-13
 // the reciprocal quotient rounds every element unless one of them lies within
 // 2^-13 of a half-integer, in which case the chunk is redone with the IEEE
 // quotient (so the codes are those of the exact quotient).
-template <int XT, int MODE>
-__device__ __forceinline__ void quant_chunk_store(const i32x4 raw, float step, float rstep, int8_t* qr, int c,
-                                                  bool store) {
+// quant_values_store: the same for E (4, 8 or 16) fp32 values already in
+// registers (chunk c of E codes).
+template <int E, int MODE>
+__device__ __forceinline__ void quant_values_store(const float (&v)[E], float step, float rstep, int8_t* qr, int c,
+                                                   bool store) {
 #pragma clang fp contract(off)
-  constexpr int E = 16 / XType<XT>::size;
-  float v[E];
-  decode_chunk<XT>(raw, v);
   uint32_t b[E];
   float dmax = 0.0f;
 #pragma unroll
@@ -107,6 +106,15 @@ __device__ __forceinline__ void quant_chunk_store(const i32x4 raw, float step, f
     else if constexpr (E == 8) reinterpret_cast<uint2*>(qr)[c] = make_uint2(packed[0], packed[1]);
     else reinterpret_cast<uint4*>(qr)[c] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
   }
+}
+
+template <int XT, int MODE>
+__device__ __forceinline__ void quant_chunk_store(const i32x4 raw, float step, float rstep, int8_t* qr, int c,
+                                                  bool store) {
+  constexpr int E = 16 / XType<XT>::size;
+  float v[E];
+  decode_chunk<XT>(raw, v);
+  quant_values_store<E, MODE>(v, step, rstep, qr, c, store);
 }
 
 }  // namespace

@@ -235,6 +235,123 @@ __global__ __launch_bounds__(256) void k_rot_quant_rows(const char* x, int64_t x
   if (t == 0) step_out[row] = step;
 }
 
+// Register-resident form of k_rot_quant_rows for K a multiple of 512 (up to
+// QG_ROT_MAX_K) and groups of 8 to 512: one row per workgroup of NW = min(8,
+// K / 512) waves; lane t of the workgroup holds, in each of NS slots, the 8
+// consecutive values 8 (s 64 NW + t) .. + 7 of the row as fp32. A group of G
+// values is G / 8 consecutive lanes of one slot (aligned), so the butterfly
+// stages h = 1, 2, 4 pair registers of a lane, and the stages h = 8 .. G / 2
+// pair register e of lanes h / 8 apart (__shfl_xor): the lower element of a
+// pair becomes a + c and the upper a - c, with a the lower and c the upper
+// value — the operations, operands and stage order of the LDS form, so the
+// results are the same bits. Lanes past K hold zeros (whole groups, K % G ==
+// 0) and store nothing. Then the scale by fp32(1 / sqrt(G)), the row's absmax
+// (wave reduction, one LDS exchange) and the shared quantizer of
+// k_quant_rows_reg (reciprocal quotient, IEEE redo near half-integers).
+template <int XT, int MODE, int NS>
+__global__ __launch_bounds__(512) void k_rot_quant_rows_reg(const char* x, int64_t x_sm, int K, int G,
+                                                            float inv_sqrt_g, int8_t* q, int64_t q_sm, int k_pad,
+                                                            float* step_out) {
+#pragma clang fp contract(off)
+  constexpr int ES = XType<XT>::size;
+  __shared__ float s_amax[8];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int nt = blockDim.x;
+  const int row = blockIdx.x;
+  const char* xr = x + static_cast<int64_t>(row) * x_sm * ES;
+  int8_t* qr = q + static_cast<int64_t>(row) * q_sm;
+  float v[NS][8];
+  bool live[NS];
+  // loads of every slot first, then their decoding
+  i32x4 raw[NS][ES == 4 ? 2 : 1];
+  static_for<0, NS>([&](auto s_c) {
+    constexpr int S = decltype(s_c)::value;
+    const int base = 8 * (S * nt + t);
+    live[S] = base < K;
+    const int b = live[S] ? base : 0;  // lanes past K read the row's first values (unused)
+    static_for<0, (ES == 4 ? 2 : 1)>([&](auto h) {
+      raw[S][decltype(h)::value] =
+          *reinterpret_cast<const i32x4*>(xr + static_cast<int64_t>(b) * ES + 16 * decltype(h)::value);
+    });
+  });
+  static_for<0, NS>([&](auto s_c) {
+    constexpr int S = decltype(s_c)::value;
+    if constexpr (ES == 4) {
+      decode_chunk<XT>(raw[S][0], v[S]);
+      decode_chunk<XT>(raw[S][1], v[S] + 4);
+    } else {
+      decode_chunk<XT>(raw[S][0], v[S]);
+    }
+    if (!live[S]) {
+      static_for<0, 8>([&](auto e) { v[S][decltype(e)::value] = 0.0f; });
+    }
+  });
+  // butterflies inside a lane: h = 1, 2, 4
+  static_for<0, NS>([&](auto s_c) {
+    constexpr int S = decltype(s_c)::value;
+    static_for<0, 3>([&](auto lh_c) {
+      constexpr int h = 1 << decltype(lh_c)::value;
+      if (h < G) {
+        static_for<0, 8>([&](auto i_c) {
+          constexpr int i = decltype(i_c)::value;
+          if constexpr ((i & h) == 0) {
+            const float a = v[S][i], c = v[S][i + h];
+            v[S][i] = a + c;
+            v[S][i + h] = a - c;
+          }
+        });
+      }
+    });
+  });
+  // butterflies across lanes: h = 8 d for lane distance d = 1 .. G / 16
+  for (int d = 1; 8 * d < G; d <<= 1) {
+    const bool upper = (lane & d) != 0;
+    static_for<0, NS>([&](auto s_c) {
+      constexpr int S = decltype(s_c)::value;
+      static_for<0, 8>([&](auto e_c) {
+        constexpr int e = decltype(e_c)::value;
+        const float self = v[S][e];
+        const float other = __shfl_xor(self, d, 64);
+        v[S][e] = upper ? other - self : self + other;
+      });
+    });
+  }
+  float amax = 0.0f;
+  static_for<0, NS>([&](auto s_c) {
+    constexpr int S = decltype(s_c)::value;
+    static_for<0, 8>([&](auto e_c) {
+      constexpr int e = decltype(e_c)::value;
+      const float r = v[S][e] * inv_sqrt_g;
+      v[S][e] = r;
+      amax = fmaxf(amax, fabsf(r));
+    });
+  });
+  amax = wave_max(amax);
+  if (lane == 0) s_amax[wave] = amax;
+  __syncthreads();
+  amax = s_amax[0];
+  for (int w = 1; w < nt / 64; ++w) amax = fmaxf(amax, s_amax[w]);
+  const float step = fmaxf(amax / 127.0f, 1.0e-20f);
+  const float rstep = __builtin_amdgcn_rcpf(step);
+  static_for<0, NS>([&](auto s_c) {
+    constexpr int S = decltype(s_c)::value;
+    quant_values_store<8, MODE>(v[S], step, rstep, qr, S * nt + t, live[S]);
+  });
+  for (int k = K + t; k < k_pad; k += nt) qr[k] = 0;
+  if (t == 0) step_out[row] = step;
+}
+
+// The register form's contract (K % 512 == 0, groups 8 .. 512, 16-byte
+// aligned rows); its slot count per lane.
+inline int rot_reg_slots(const void* x, int x_dtype, int64_t x_sm, int64_t K, int G, int8_t* q, int64_t q_sm) {
+  const int es = x_dtype == QG_F32 ? 4 : 2;
+  if (K % 512 != 0 || K > QG_ROT_MAX_K || G < 8 || G > 512) return 0;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_sm * es) % 16 != 0) return 0;
+  if ((reinterpret_cast<uintptr_t>(q) & 7) != 0 || q_sm % 8 != 0) return 0;
+  const int64_t nw = K / 512 < 8 ? K / 512 : 8;
+  return static_cast<int>((K + 512 * nw - 1) / (512 * nw));
+}
+
 template <int MODE>
 hipError_t launch_rot_quant_mode(const void* x, int x_dtype, int64_t x_sm, int64_t M, int64_t K, int G,
                                  float inv_sqrt_g, int8_t* q, int64_t q_sm, int64_t k_pad, float* step,
@@ -242,6 +359,26 @@ hipError_t launch_rot_quant_mode(const void* x, int x_dtype, int64_t x_sm, int64
   const dim3 grid(static_cast<unsigned>(M));
   const char* xp = static_cast<const char*>(x);
   const int k = static_cast<int>(K), kp = static_cast<int>(k_pad);
+  const int ns = rot_reg_slots(x, x_dtype, x_sm, K, G, q, q_sm);
+  if (ns > 0) {
+    const dim3 block(static_cast<unsigned>(64 * (K / 512 < 8 ? K / 512 : 8)));
+#define QG_ROT_REG(XT, NS)                                                                                      \
+  hipLaunchKernelGGL((k_rot_quant_rows_reg<XT, MODE, NS>), grid, block, 0, stream, xp, x_sm, k, G, inv_sqrt_g, q, \
+                     q_sm, kp, step)
+#define QG_ROT_REG_NS(XT)                  \
+  do {                                     \
+    if (ns == 1) QG_ROT_REG(XT, 1);        \
+    else if (ns == 2) QG_ROT_REG(XT, 2);   \
+    else if (ns == 3) QG_ROT_REG(XT, 3);   \
+    else QG_ROT_REG(XT, 4);                \
+  } while (0)
+    if (x_dtype == QG_F32) QG_ROT_REG_NS(QG_F32);
+    else if (x_dtype == QG_F16) QG_ROT_REG_NS(QG_F16);
+    else QG_ROT_REG_NS(QG_BF16);
+#undef QG_ROT_REG_NS
+#undef QG_ROT_REG
+    return hipGetLastError();
+  }
   switch (x_dtype) {
     case QG_F32:
       hipLaunchKernelGGL((k_rot_quant_rows<QG_F32, MODE>), grid, dim3(256), 0, stream, xp, x_sm, k, G, inv_sqrt_g, q,

@@ -41,7 +41,8 @@ def _rows(shape, seed):
 
 @pytest.mark.parametrize("dtype", FLOATS)
 @pytest.mark.parametrize("g,shape", [(256, (1061, 3072)), (2, (5, 6)), (4, (33, 12)), (16, (7, 112)),
-                                     (128, (3, 4096)), (1024, (9, 16384)), (256, (1, 256)), (512, (17, 1536))])
+                                     (128, (3, 4096)), (1024, (9, 16384)), (256, (1, 256)), (512, (17, 1536)),
+                                     (8, (5, 512)), (16, (9, 2048)), (64, (2, 12288)), (32, (3, 16384))])
 def test_rot_quant_rows_bit_exact(cuda, dtype, g, shape):
     from rdna2_ops.quantize import rotate_quantize_int8_rowwise
     case(f"rot quant {dtype} g{g} {shape}")
@@ -152,6 +153,33 @@ def test_w8a8_linear_residual_moss_shape(cuda, out):
     plain_g = w8a8_linear(x, w, ws, bias, out_dtype=torch.float32, activation="gelu_tanh")
     fused_g = w8a8_linear(x, w, ws, bias, out_dtype=torch.float32, activation="gelu_tanh", residual=res)
     assert torch.equal(fused_g, plain_g + res)
+
+
+@pytest.mark.parametrize("m,n,k,pad", [(1061, 9216, 3072, 0), (1100, 9002, 256, 3)])
+def test_w8a8_linear_residual_pingpong_grid(cuda, m, n, k, pad):
+    """Grids of >= 192 tiles of 256 x 192 run the residual epilogue on the
+    persistent ping-pong kernel: for every output / residual dtype and scale
+    kind the fused output equals the plain linear's fp32 value plus
+    f32(residual) (x scale), rounded once — including a ragged N (edge tiles)
+    and a residual row stride that is not a multiple of 4 (unaligned rows:
+    element-wise residual loads)."""
+    from rdna2_ops.int8_gemm import w8a8_linear
+    x = _rows((m, k), 15).to(cuda)
+    w, ws, bias = (t.to(cuda) for t in _weights(n, k, 16))
+    gen = torch.Generator().manual_seed(17)
+    plain = w8a8_linear(x, w, ws, bias, out_dtype=torch.float32)
+    for rdt in FLOATS:
+        base = (torch.randn(m, n + pad, generator=gen) * 2).to(rdt).to(cuda)
+        res = base[:, :n]
+        for scale_kind in ("none", "scalar", "channel"):
+            rs = {"none": None, "scalar": torch.tensor([0.75], device=cuda),
+                  "channel": (torch.rand(n, generator=gen) + 0.25).to(cuda)}[scale_kind]
+            term = res.float() if rs is None else res.float() * rs
+            for out in FLOATS:
+                case(f"w8a8 residual ping-pong {m}x{n}x{k} res={rdt} scale={scale_kind} out={out}")
+                fused = w8a8_linear(x, w, ws, bias, out_dtype=out, residual=res, residual_scale=rs)
+                want = (plain + term).to(out)
+                assert np.array_equal(bits(fused), bits(want)), (rdt, scale_kind, out)
 
 
 def test_w8a8_linear_convrot_end_to_end_against_dense(cuda):

@@ -299,8 +299,7 @@ def test_cfg1_chain_stages(cuda, stage):
 def test_cfg1_chain_end_to_end(cuda):
     """BASELINE config 1 end to end on the GPU (QKV, then MLP up + GELU-tanh,
     whose fp16 output feeds the down projection), against the oracle chain on
-    96 rows spread over the 4096 tokens (every stage is row-independent).
-    QKV is bit-exact. The down projection's input differs from the oracle's
+    all 4096 tokens. QKV is bit-exact. The down projection's input differs from the oracle's
     by at most one fp16 ulp (GELU through the hardware exp2 / reciprocal), so
     the final output is held to the BASELINE bar (1e-2 x RMS plus half an fp16
     ulp) and to RMS(error) <= 2e-3 x RMS."""
@@ -317,16 +316,16 @@ def test_cfg1_chain_end_to_end(cuda):
     h = w8a8_linear(x, wq_up, ws_up, c.b_up.to(cuda), activation="gelu_tanh")
     y = w8a8_linear(h, wq_dn, ws_dn, c.b_down.to(cuda))
     assert torch.isfinite(y).all()
-    rows = np.linspace(0, c.x.shape[0] - 1, 96).astype(int)
-    xr = c.x.float().numpy()[rows]
+    xr = c.x.float().numpy()
     ref_qkv, _, _, _ = o.w8a8_linear(xr, wq_qkv.cpu().numpy(), ws_qkv.cpu().numpy().reshape(-1),
                                      c.b_qkv.float().numpy(), out="f16")
-    assert np.array_equal(f16_bits(qkv[torch.from_numpy(rows).to(cuda)]), o.encode(ref_qkv, "f16").view(np.int16))
+    assert np.array_equal(f16_bits(qkv), o.encode(ref_qkv, "f16").view(np.int16))
+    del ref_qkv
     ref_h, _, _, _ = o.w8a8_linear(xr, wq_up.cpu().numpy(), ws_up.cpu().numpy().reshape(-1),
                                    c.b_up.float().numpy(), out="f16", activation="gelu_tanh")
     ref_y, _, _, _ = o.w8a8_linear(o.round_to(ref_h, "f16"), wq_dn.cpu().numpy(), ws_dn.cpu().numpy().reshape(-1),
                                    c.b_down.float().numpy(), out="f16")
-    got = y[torch.from_numpy(rows).to(cuda)].float().cpu().numpy().astype(np.float64)
+    got = y.float().cpu().numpy().astype(np.float64)
     exp = np.asarray(ref_y, np.float64)
     err = np.abs(got - exp)
     rms = float(np.sqrt(np.mean(exp ** 2)))

@@ -81,15 +81,25 @@ __device__ __forceinline__ int a_frag_offset(int t, int lane) {
 }
 
 // Weight registers of one stage: 4 k-steps of a lane's 16 K bytes (2 packed
-// words, or 16 prepared bytes), and the stage's per-group unsigned zero points
-// replicated into the 4 bytes of a dword.
+// words, or 16 prepared bytes), and the stage's per-group zero points as
+// loaded (the packed word or the int32), decoded only where the stage
+// computes so that no wait for these loads is needed before then.
 template <bool PREP>
 struct WStage {
   uint32_t w[4][PREP ? 4 : 2];
-  uint32_t zb[4];
+  uint32_t zraw[4];
 };
+template <bool PREP>
+__device__ __forceinline__ void settle_stage(WStage<PREP>& b) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int e = 0; e < (PREP ? 4 : 2); ++e) asm volatile("" : "+v"(b.w[t][e]));
+    if constexpr (!PREP) asm volatile("" : "+v"(b.zraw[t]));
+  }
+}
 
-template <int G, bool PREP, bool INTEGER, int NW, bool VEC>
+template <int G, bool PREP, bool INTEGER, int NW, bool VEC, bool FULLK>
 __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
 #pragma clang fp contract(off)
   constexpr int GK = G / 32;      // k-steps per group
@@ -121,7 +131,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
               static_cast<uint32_t>(p.a_sm);
   const char* a_base = reinterpret_cast<const char*>(p.a);
   auto copy_a = [&](int s, int slot) __attribute__((always_inline)) {
-    const uint32_t ch = (s == S - 1 && chunk >= klast) ? 0u : chunk;
+    const uint32_t ch = (!FULLK && s == S - 1 && chunk >= klast) ? 0u : chunk;
 #pragma unroll
     for (int i = 0; i < NA; ++i)
       dma16s(a_base + static_cast<int64_t>(s) * kStage, aoff[i] + ch,
@@ -172,43 +182,51 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
       static_for<0, GS>([&](auto gi_c) {
         constexpr int gi = decltype(gi_c)::value;
         const int g = min(s * GS + gi, p.ng - 1);
-        int zu;
-        if (zpk) {
-          const uint32_t zword = static_cast<const uint32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.zw + (g >> 3)];
-          const int z = static_cast<int>((zword >> (4 * (g & 7))) & 15u);
-          zu = sgn ? (z ^ 8) : z;
-        } else {
-          const int z = static_cast<const int32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.ng + g];
-          zu = sgn ? z + 8 : z;
-        }
-        b.zb[gi] = static_cast<uint32_t>(zu) * 0x01010101u;
+        b.zraw[gi] = zpk ? static_cast<const uint32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.zw + (g >> 3)]
+                         : static_cast<uint32_t>(static_cast<const int32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.ng + g]);
       });
     }
+  };
+  // Group gi of stage s: the unsigned zero point of this lane's row replicated
+  // into the 4 bytes of a dword.
+  auto zero_bytes = [&](int s, int gi, uint32_t zraw) __attribute__((always_inline)) {
+    const int g = min(s * GS + gi, p.ng - 1);
+    int zu;
+    if (zpk) {
+      const int z = static_cast<int>((zraw >> (4 * (g & 7))) & 15u);
+      zu = sgn ? (z ^ 8) : z;
+    } else {
+      const int z = static_cast<int>(zraw);
+      zu = sgn ? z + 8 : z;
+    }
+    return static_cast<uint32_t>(zu) * 0x01010101u;
   };
 
   // ---- scales of a stage: thread t covers column t % BN and the stage's
   // groups t / BN and t / BN + 2 (clamped; only valid ones are stored)
   const int scol = tid & (kBN - 1), sg0 = tid / kBN;
   const int scn = min(n0 + scol, p.N - 1);
-  auto load_scales = [&](int s, float (&sc)[2]) __attribute__((always_inline)) {
+  // (the raw bits are kept until parked: a bf16 value is widened there, so
+  // nothing waits for these loads before the stage's MFMAs)
+  auto load_scales = [&](int s, uint32_t (&sc)[2]) __attribute__((always_inline)) {
     if constexpr (!INTEGER) {
       static_for<0, 2>([&](auto j_c) {
         constexpr int j = decltype(j_c)::value;
         const int gi = min(sg0 + 2 * j, GS - 1);
         const int g = min(s * GS + gi, p.ng - 1);
         const int64_t i = static_cast<int64_t>(scn) * p.ng + g;
-        sc[j] = p.scale_f32 ? static_cast<const float*>(p.scales)[i]
-                            : bf16_to_f32(static_cast<const uint16_t*>(p.scales)[i]);
+        sc[j] = p.scale_f32 ? static_cast<const uint32_t*>(p.scales)[i]
+                            : static_cast<uint32_t>(static_cast<const uint16_t*>(p.scales)[i]);
       });
     }
   };
-  auto park_scales = [&](int slot, const float (&sc)[2]) __attribute__((always_inline)) {
+  auto park_scales = [&](int slot, const uint32_t (&sc)[2]) __attribute__((always_inline)) {
     if constexpr (!INTEGER) {
       float* dst = reinterpret_cast<float*>(smem + 2 * kSlotA + slot * kSlotS);
       static_for<0, 2>([&](auto j_c) {
         constexpr int j = decltype(j_c)::value;
         const int gi = sg0 + 2 * j;
-        if (gi < GS) dst[gi * kBN + scol] = sc[j];
+        if (gi < GS) dst[gi * kBN + scol] = p.scale_f32 ? __uint_as_float(sc[j]) : bf16_to_f32(static_cast<uint16_t>(sc[j]));
       });
     }
   };
@@ -226,17 +244,27 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
   // Fold the finished group gi of the stage in slot `slot` into the totals.
   auto flush = [&](int slot, int gi) __attribute__((always_inline)) {
     const float* scl = reinterpret_cast<const float*>(smem + 2 * kSlotA + slot * kSlotS) + gi * kBN;
+    f32x4 s4q[4];
+    static_for<0, 4>([&](auto q) {
+      s4q[q] = f32x4{0, 0, 0, 0};
+      if constexpr (!INTEGER) s4q[q] = *reinterpret_cast<const f32x4*>(scl + 32 * wave + 8 * q + 4 * h);
+    });
     static_for<0, 4>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
       static_for<0, 4>([&](auto q_c) {
         constexpr int q = decltype(q_c)::value;
-        f32x4 s4 = {0, 0, 0, 0};
-        if constexpr (!INTEGER) s4 = *reinterpret_cast<const f32x4*>(scl + 32 * wave + 8 * q + 4 * h);
+        const f32x4 s4 = s4q[q];
         static_for<0, 4>([&](auto c_c) {
           constexpr int c = decltype(c_c)::value;
           const int v = acc[i][4 * q + c];
           if constexpr (INTEGER) itot[i][4 * q + c] += v;
           else tot[i][4 * q + c] = tot[i][4 * q + c] + static_cast<float>(v) * s4[c];
+          // Pin the fold here: otherwise instruction selection may defer it
+          // past the next group's MFMAs, keeping every group's sums live.
+          if constexpr (FULLK) {
+            if constexpr (INTEGER) asm volatile("" : "+v"(itot[i][4 * q + c]));
+            else asm volatile("" : "+v"(tot[i][4 * q + c]));
+          }
         });
       });
     });
@@ -251,6 +279,8 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
     // 4 t + 2 h, + 1. Each half keeps the pairs it holds and swaps the other
     // two with the lane 32 away.
     WStage<PREP> b = b_in;
+    uint32_t zbs[GS];
+    if constexpr (!PREP) static_for<0, GS>([&](auto gi) { zbs[gi] = zero_bytes(s, gi, b_in.zraw[gi]); });
     if constexpr (VEC) {
       const uint32_t* r = &b_in.w[0][0];  // r[0..3] = first load, r[4..7] = second
       uint32_t snd[4], got[4];
@@ -268,46 +298,78 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
       b.w[3][0] = h ? r[6] : got[2];
       b.w[3][1] = h ? r[7] : got[3];
     }
-    static_for<0, 4>([&](auto t_c) {
+    auto read_a = [&](auto t_c, i32x4 (&af)[4]) __attribute__((always_inline)) {
       constexpr int t = decltype(t_c)::value;
-      if (s * 4 + t < KT) {
-        i32x4 af[4];
-        static_for<0, 4>([&](auto i_c) {
-          constexpr int i = decltype(i_c)::value;
-          af[i] = *reinterpret_cast<const i32x4*>(abase + i * 32 * kStage + a_frag_offset(t, lane));
-        });
-        i32x4 wf;
-        if constexpr (PREP) {
-          wf = i32x4{static_cast<int>(b.w[t][0]), static_cast<int>(b.w[t][1]), static_cast<int>(b.w[t][2]),
+      static_for<0, 4>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value;
+        af[i] = *reinterpret_cast<const i32x4*>(abase + i * 32 * kStage + a_frag_offset(t, lane));
+      });
+    };
+    // k-step t's weight fragment: 16 bytes of q - z (or the prepared bytes)
+    auto weight_frag = [&](auto t_c) __attribute__((always_inline)) {
+      constexpr int t = decltype(t_c)::value;
+      if constexpr (PREP) {
+        return i32x4{static_cast<int>(b.w[t][0]), static_cast<int>(b.w[t][1]), static_cast<int>(b.w[t][2]),
                      static_cast<int>(b.w[t][3])};
-        } else {
-          const uint32_t zb = b.zb[t / GK];
-          auto expand = [&](uint32_t word, uint32_t& d0, uint32_t& d1) __attribute__((always_inline)) {
-            const uint32_t x = word ^ xmask;
-            const uint32_t lo = (((x & 0x0F0F0F0Fu) | 0x80808080u) - zb) ^ 0x80808080u;
-            const uint32_t hi = ((((x >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zb) ^ 0x80808080u;
-            d0 = __builtin_amdgcn_perm(hi, lo, sel0);
-            d1 = __builtin_amdgcn_perm(hi, lo, sel1);
-          };
-          uint32_t d[4];
-          expand(b.w[t][0], d[0], d[1]);
-          expand(b.w[t][1], d[2], d[3]);
-          wf = i32x4{static_cast<int>(d[0]), static_cast<int>(d[1]), static_cast<int>(d[2]), static_cast<int>(d[3])};
-        }
-        static_for<0, 4>([&](auto i_c) {
-          constexpr int i = decltype(i_c)::value;
-          if constexpr (t % GK == 0) acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, af[i], i32x16{}, 0, 0, 0);
-          else acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, af[i], acc[i], 0, 0, 0);
-        });
-        if constexpr ((t + 1) % GK == 0) flush(slot, t / GK);
+      } else {
+        const uint32_t zb = zbs[t / GK];
+        auto expand = [&](uint32_t word, uint32_t& d0, uint32_t& d1) __attribute__((always_inline)) {
+          const uint32_t x = word ^ xmask;
+          const uint32_t lo = (((x & 0x0F0F0F0Fu) | 0x80808080u) - zb) ^ 0x80808080u;
+          const uint32_t hi = ((((x >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zb) ^ 0x80808080u;
+          d0 = __builtin_amdgcn_perm(hi, lo, sel0);
+          d1 = __builtin_amdgcn_perm(hi, lo, sel1);
+        };
+        uint32_t d[4];
+        expand(b.w[t][0], d[0], d[1]);
+        expand(b.w[t][1], d[2], d[3]);
+        return i32x4{static_cast<int>(d[0]), static_cast<int>(d[1]), static_cast<int>(d[2]), static_cast<int>(d[3])};
       }
-    });
+    };
+    auto mfmas = [&](auto t_c, const i32x4& wf, const i32x4 (&af)[4]) __attribute__((always_inline)) {
+      constexpr int t = decltype(t_c)::value;
+      static_for<0, 4>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value;
+        if constexpr (t % GK == 0) acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, af[i], i32x16{}, 0, 0, 0);
+        else acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, af[i], acc[i], 0, 0, 0);
+      });
+    };
+    if constexpr (FULLK) {
+      // Four k-steps, software-pipelined by hand: k-step t + 1's A fragments
+      // are read and its weight fragment expanded while k-step t's MFMAs run,
+      // and nothing moves across k-steps (the compiler would otherwise hoist
+      // every read of the stage and run out of registers).
+      i32x4 af[2][4];
+      read_a(std::integral_constant<int, 0>{}, af[0]);
+      i32x4 wf = weight_frag(std::integral_constant<int, 0>{});
+      static_for<0, 4>([&](auto t_c) {
+        constexpr int t = decltype(t_c)::value;
+        i32x4 wn = wf;
+        if constexpr (t + 1 < 4) read_a(std::integral_constant<int, t + 1>{}, af[(t + 1) & 1]);
+        mfmas(t_c, wf, af[t & 1]);
+        if constexpr (t + 1 < 4) wn = weight_frag(std::integral_constant<int, t + 1>{});
+        if constexpr ((t + 1) % GK == 0) flush(slot, t / GK);
+        wf = wn;
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    } else {
+      static_for<0, 4>([&](auto t_c) {
+        constexpr int t = decltype(t_c)::value;
+        if (s * 4 + t < KT) {
+          i32x4 af[4];
+          read_a(t_c, af);
+          const i32x4 wf = weight_frag(t_c);
+          mfmas(t_c, wf, af);
+          if constexpr ((t + 1) % GK == 0) flush(slot, t / GK);
+        }
+      });
+    }
   };
 
   // ---- pipeline: stage s + 1's copies and loads are issued before stage s
   // computes; one barrier per stage.
   WStage<PREP> wb[2];
-  float sc[2] = {0.0f, 0.0f};
+  uint32_t sc[2] = {0u, 0u};
   copy_a(0, 0);
   load_w(0, wb[0]);
   load_scales(0, sc);
@@ -316,6 +378,12 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
   wait_lds_barrier();
   auto stage = [&](int s, auto cur_c) __attribute__((always_inline)) {
     constexpr int cur = decltype(cur_c)::value;
+    // This stage's weight registers landed before the last barrier (its wait
+    // is inline assembly, which the compiler's wait insertion cannot see):
+    // touch them before the next stage's loads are issued, so that the
+    // compiler's own wait for them falls here, where it is free, and not
+    // behind the new loads.
+    settle_stage(wb[cur]);
     if (s + 1 < S) {
       copy_a(s + 1, (s + 1) & 1);
       load_w(s + 1, wb[cur ^ 1]);
@@ -335,14 +403,43 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
   }
   if (s < S) stage(s, std::integral_constant<int, 0>{});
 
-  // ---- output: row m0 + 32 i + (l & 31), columns n0 + 32 wave + 8 q + 4 h + c
+  // ---- output: row m0 + 32 i + (l & 31), columns n0 + 32 wave + 8 q + 4 h + c.
+  // The row scales and the bias values are loaded before the first store (a
+  // load after a store to a possibly aliasing address would wait for it).
   const bool vec = (p.N % 4) == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+  float sa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float bv[4][4];
+  if constexpr (!INTEGER) {
+    static_for<0, 4>([&](auto i) { sa[i] = p.a_scale[min(m0 + 32 * decltype(i)::value + lr, p.M - 1)]; });
+    // all raw values first, then the widening (no wait between loads)
+    uint32_t braw[4][4] = {};
+    auto bias_cols = [&](auto load) __attribute__((always_inline)) {
+      static_for<0, 4>([&](auto q_c) {
+        constexpr int q = decltype(q_c)::value;
+        static_for<0, 4>([&](auto c_c) {
+          constexpr int c = decltype(c_c)::value;
+          braw[q][c] = load(min(n0 + 32 * wave + 8 * q + 4 * h + c, p.N - 1));
+        });
+      });
+    };
+    if (p.bias != nullptr) {
+      if (p.bias_dtype == QG_F32) bias_cols([&](int col) { return static_cast<const uint32_t*>(p.bias)[col]; });
+      else bias_cols([&](int col) { return static_cast<uint32_t>(static_cast<const uint16_t*>(p.bias)[col]); });
+    }
+    static_for<0, 4>([&](auto q) {
+      static_for<0, 4>([&](auto c) {
+        const uint32_t r = braw[decltype(q)::value][decltype(c)::value];
+        bv[q][c] = p.bias_dtype == QG_F32   ? __uint_as_float(r)
+                   : p.bias_dtype == QG_F16 ? f16_to_f32(static_cast<uint16_t>(r))
+                                            : bf16_to_f32(static_cast<uint16_t>(r));
+      });
+    });
+  }
+  const bool has_bias = p.bias != nullptr;
   static_for<0, 4>([&](auto i_c) {
     constexpr int i = decltype(i_c)::value;
     const int row = m0 + 32 * i + lr;
     if (row >= p.M) return;
-    float sa = 0.0f;
-    if constexpr (!INTEGER) sa = p.a_scale[row];
     static_for<0, 4>([&](auto q_c) {
       constexpr int q = decltype(q_c)::value;
       const int col0 = n0 + 32 * wave + 8 * q + 4 * h;
@@ -352,15 +449,8 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
         if constexpr (INTEGER) {
           bits[c] = static_cast<uint32_t>(itot[i][4 * q + c]);
         } else {
-          float y = tot[i][4 * q + c] * sa;
-          if (p.bias != nullptr) {
-            const int col = min(col0 + c, p.N - 1);
-            float bv;
-            if (p.bias_dtype == QG_F32) bv = static_cast<const float*>(p.bias)[col];
-            else if (p.bias_dtype == QG_F16) bv = f16_to_f32(static_cast<const uint16_t*>(p.bias)[col]);
-            else bv = bf16_to_f32(static_cast<const uint16_t*>(p.bias)[col]);
-            y = y + bv;
-          }
+          float y = tot[i][4 * q + c] * sa[i];
+          if (has_bias) y = y + bv[q][c];
           bits[c] = __float_as_uint(y);
         }
       });
@@ -392,14 +482,24 @@ hipError_t launch_g(const W4A8Args& p, hipStream_t stream) {
   // nk words with 16-byte aligned rows (K % 32 == 0 makes every row a
   // multiple of 16 bytes): 16-byte weight loads
   const bool vec = !PREP && !(p.flags & QG_W4_LAYOUT_KN) && (reinterpret_cast<uintptr_t>(p.w) & 15) == 0;
+  // K a multiple of the 128-byte stage: every stage holds four k-steps, and
+  // the stage body is one straight-line block the compiler can schedule
+  // across k-steps (fragment reads and nibble expansion under the MFMAs)
+  const bool fullk = (p.K % kStage) == 0;
   const dim3 grid(blocks), block(W8Geo<NW>::THREADS);
+#define QG_W4A8(INT, V)                                                                                 \
+  do {                                                                                                \
+    if (fullk) hipLaunchKernelGGL((k_w4a8<G, PREP, INT, NW, V, true>), grid, block, 0, stream, p);   \
+    else hipLaunchKernelGGL((k_w4a8<G, PREP, INT, NW, V, false>), grid, block, 0, stream, p);        \
+  } while (0)
   if (p.integer) {
-    if (vec) hipLaunchKernelGGL((k_w4a8<G, PREP, true, NW, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((k_w4a8<G, PREP, true, NW, false>), grid, block, 0, stream, p);
+    if (vec) QG_W4A8(true, true);
+    else QG_W4A8(true, false);
   } else {
-    if (vec) hipLaunchKernelGGL((k_w4a8<G, PREP, false, NW, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((k_w4a8<G, PREP, false, NW, false>), grid, block, 0, stream, p);
+    if (vec) QG_W4A8(false, true);
+    else QG_W4A8(false, false);
   }
+#undef QG_W4A8
   return hipGetLastError();
 }
 

@@ -469,6 +469,285 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
   });
 }
 
+// ---- waves of 128 rows x 16 columns (K a multiple of 128, packed weights)
+//
+// The same arithmetic and fold order as k_w4a8 on v_mfma_i32_16x16x32_i8:
+// wave w owns output columns 16 w .. 16 w + 15 of a 128 x 16 NW tile over all
+// 128 rows (eight 16 x 16 int32 blocks, weights as the first operand). Half
+// the columns per wave keeps the nibble expansion and fold per MAC and
+// doubles the LDS fragment reads; at <= 168 registers three 4-wave
+// workgroups share a CU, so a grid too small to fill the CUs with the 4-wave
+// form's 128 x 128 tiles gets twice the tiles and up to three independent
+// waves per SIMD (waves of one workgroup meet at every stage's barrier and so
+// run their folds and MFMAs in step: an 8-wave form measured slower).
+//
+// A k-step is 32 K (one g32 group, half a g64 one, a quarter of g128): lane
+// l = 16 kg + c supplies 8 bytes of K [32 t + 8 kg, 32 t + 8 kg + 8) of
+// weight column 16 w + c (one packed word, expanded to q - z) and of
+// activation row 16 b + c; the block result holds columns 16 w + 4 kg .. + 3
+// of row 16 b + c in its 4 registers.
+template <int G, bool INTEGER, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_w4a8_n16(W4A8Args p) {
+#pragma clang fp contract(off)
+  constexpr int BN = 16 * NW;                  // 64 or 128 columns
+  constexpr int GK = G / 32;                   // k-steps per group
+  constexpr int GS = kStage / G;               // groups per stage
+  constexpr int NA = 16 / NW;                  // A copies (1 KB) per wave and stage
+  constexpr int SLOT_S = 4 * BN * 4;           // <= 4 groups x BN fp32 scales
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kSlotA + 2 * SLOT_S];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, kg = lane >> 4;
+  int m0, n0;
+  w4a8_tile<BN>(p.M, p.N, m0, n0);
+  const int S = p.K / kStage;                  // the launcher guarantees K % 128 == 0
+  const uint32_t smem_base = lds_addr_of(smem);
+
+  // ---- A copies: as k_w4a8 (rows 8 (wave + NW i) + (l >> 3), chunk swizzle)
+  const uint32_t chunk = static_cast<uint32_t>(((lane & 7) ^ (4 * (wave & 1) + (lane >> 4))) << 4);
+  uint32_t aoff[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+    aoff[i] = static_cast<uint32_t>(min(m0 + wave * 8 + (lane >> 3) + 8 * NW * i, p.M - 1)) *
+              static_cast<uint32_t>(p.a_sm);
+  const char* a_base = reinterpret_cast<const char*>(p.a);
+  auto copy_a = [&](int s, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+      dma16s(a_base + static_cast<int64_t>(s) * kStage, aoff[i] + chunk, smem_base + slot * kSlotA + (wave + NW * i) * 1024);
+  };
+
+  // ---- this lane's weight column and its packed words: k-step t of stage s
+  // is word 16 s + 4 t + kg of the column (nk: consecutive words of a row;
+  // kn: words N apart)
+  const int nw = min(n0 + 16 * wave + c16, p.N - 1);
+  const bool kn = p.flags & QG_W4_LAYOUT_KN;
+  const bool sgn = p.flags & QG_W4_SIGNED_NIBBLES;
+  const bool zpk = p.flags & QG_W4_ZEROS_PACKED;
+  const bool high = p.flags & QG_W4_ORDER_HIGH;
+  const uint32_t* wcol = p.w + (kn ? static_cast<int64_t>(nw) : static_cast<int64_t>(nw) * (p.K / 8));
+  const int64_t kstride = kn ? p.N : 1;
+  const uint32_t xmask = sgn ? 0x88888888u : 0u;
+  const uint32_t sel0 = high ? 0x02060307u : 0x05010400u;
+  const uint32_t sel1 = high ? 0x00040105u : 0x07030602u;
+
+  struct Stage {
+    uint32_t w[4];
+    uint32_t zraw[4];
+  };
+  auto load_w = [&](int s, Stage& b) __attribute__((always_inline)) {
+    static_for<0, 4>([&](auto t) { b.w[decltype(t)::value] = wcol[(16 * s + 4 * decltype(t)::value + kg) * kstride]; });
+    static_for<0, GS>([&](auto gi_c) {
+      constexpr int gi = decltype(gi_c)::value;
+      const int g = min(s * GS + gi, p.ng - 1);
+      b.zraw[gi] = zpk ? static_cast<const uint32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.zw + (g >> 3)]
+                       : static_cast<uint32_t>(static_cast<const int32_t*>(p.zeros)[static_cast<int64_t>(nw) * p.ng + g]);
+    });
+  };
+  auto zero_bytes = [&](int s, int gi, uint32_t zraw) __attribute__((always_inline)) {
+    const int g = min(s * GS + gi, p.ng - 1);
+    int zu;
+    if (zpk) {
+      const int z = static_cast<int>((zraw >> (4 * (g & 7))) & 15u);
+      zu = sgn ? (z ^ 8) : z;
+    } else {
+      const int z = static_cast<int>(zraw);
+      zu = sgn ? z + 8 : z;
+    }
+    return static_cast<uint32_t>(zu) * 0x01010101u;
+  };
+  // a packed word (8 K in order) -> 8 signed bytes q - z in K order
+  auto expand = [&](uint32_t word, uint32_t zb) __attribute__((always_inline)) {
+    const uint32_t x = word ^ xmask;
+    const uint32_t lo = (((x & 0x0F0F0F0Fu) | 0x80808080u) - zb) ^ 0x80808080u;
+    const uint32_t hi = ((((x >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zb) ^ 0x80808080u;
+    const uint64_t d0 = __builtin_amdgcn_perm(hi, lo, sel0);
+    const uint64_t d1 = __builtin_amdgcn_perm(hi, lo, sel1);
+    return static_cast<int64_t>(d0 | (d1 << 32));
+  };
+
+  // ---- scales of a stage: thread t covers column t % BN, group t / BN
+  const int scol = tid & (BN - 1), sg = tid / BN;
+  const int scn = min(n0 + scol, p.N - 1);
+  auto load_scales = [&](int s, uint32_t& sc) __attribute__((always_inline)) {
+    if constexpr (!INTEGER) {
+      const int g = min(s * GS + min(sg, GS - 1), p.ng - 1);
+      const int64_t i = static_cast<int64_t>(scn) * p.ng + g;
+      sc = p.scale_f32 ? static_cast<const uint32_t*>(p.scales)[i]
+                       : static_cast<uint32_t>(static_cast<const uint16_t*>(p.scales)[i]);
+    }
+  };
+  auto park_scales = [&](int slot, uint32_t sc) __attribute__((always_inline)) {
+    if constexpr (!INTEGER) {
+      float* dst = reinterpret_cast<float*>(smem + 2 * kSlotA + slot * SLOT_S);
+      if (sg < GS) dst[sg * BN + scol] = p.scale_f32 ? __uint_as_float(sc) : bf16_to_f32(static_cast<uint16_t>(sc));
+    }
+  };
+
+  i32x4 acc[8];
+  float tot[8][4];
+  int itot[8][4];
+  static_for<0, 8>([&](auto b) {
+    static_for<0, 4>([&](auto r) {
+      tot[b][r] = 0.0f;
+      itot[b][r] = 0;
+    });
+  });
+  // fold the finished group gi of the stage in slot `slot` (pinned in place,
+  // as in k_w4a8's full-K body)
+  auto flush = [&](int slot, int gi) __attribute__((always_inline)) {
+    f32x4 s4 = {0, 0, 0, 0};
+    if constexpr (!INTEGER)
+      s4 = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(smem + 2 * kSlotA + slot * SLOT_S) +
+                                           gi * BN + 16 * wave + 4 * kg);
+    static_for<0, 8>([&](auto b_c) {
+      constexpr int b = decltype(b_c)::value;
+      static_for<0, 4>([&](auto r_c) {
+        constexpr int r = decltype(r_c)::value;
+        const int v = acc[b][r];
+        if constexpr (INTEGER) {
+          itot[b][r] += v;
+          asm volatile("" : "+v"(itot[b][r]));
+        } else {
+          tot[b][r] = tot[b][r] + static_cast<float>(v) * s4[r];
+          asm volatile("" : "+v"(tot[b][r]));
+        }
+      });
+    });
+  };
+  // activation fragment of block b, k-step t: row 16 b + c16, K bytes
+  // [32 t + 8 kg, + 8) = half (kg & 1) of logical chunk 2 t + (kg >> 1)
+  auto read_a = [&](const char* abase, auto t_c, int64_t (&af)[8]) __attribute__((always_inline)) {
+    constexpr int t = decltype(t_c)::value;
+    static_for<0, 8>([&](auto b_c) {
+      constexpr int b = decltype(b_c)::value;
+      const int row = 16 * b + c16;
+      const int off = row * kStage + ((((2 * t + (kg >> 1)) ^ ((row >> 1) & 7))) << 4) + 8 * (kg & 1);
+      af[b] = *reinterpret_cast<const int64_t*>(abase + off);
+    });
+  };
+
+  // MFMAs of stage s: k-step t + 1's fragments are read and its weight word
+  // expanded under k-step t's MFMAs; nothing moves across k-steps.
+  auto compute = [&](int s, const Stage& b_in) __attribute__((always_inline)) {
+    const int slot = s & 1;
+    const char* abase = smem + slot * kSlotA;
+    uint32_t zbs[GS];
+    static_for<0, GS>([&](auto gi) { zbs[gi] = zero_bytes(s, gi, b_in.zraw[gi]); });
+    int64_t af[2][8];
+    read_a(abase, std::integral_constant<int, 0>{}, af[0]);
+    int64_t wf = expand(b_in.w[0], zbs[0]);
+    static_for<0, 4>([&](auto t_c) {
+      constexpr int t = decltype(t_c)::value;
+      int64_t wn = wf;
+      if constexpr (t + 1 < 4) read_a(abase, std::integral_constant<int, t + 1>{}, af[(t + 1) & 1]);
+      static_for<0, 8>([&](auto b_c) {
+        constexpr int b = decltype(b_c)::value;
+        if constexpr (t % GK == 0) acc[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af[t & 1][b], i32x4{}, 0, 0, 0);
+        else acc[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wf, af[t & 1][b], acc[b], 0, 0, 0);
+      });
+      if constexpr (t + 1 < 4) wn = expand(b_in.w[t + 1], zbs[(t + 1) / GK]);
+      if constexpr ((t + 1) % GK == 0) flush(slot, t / GK);
+      wf = wn;
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // ---- pipeline: stage s + 1's copies and loads are issued before stage s
+  // computes (this stage's registers touched first, see k_w4a8); one barrier
+  // per stage
+  Stage wb[2];
+  uint32_t sc = 0u;
+  copy_a(0, 0);
+  load_w(0, wb[0]);
+  load_scales(0, sc);
+  wait_vm<0>();
+  park_scales(0, sc);
+  wait_lds_barrier();
+  auto settle = [&](Stage& b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      asm volatile("" : "+v"(b.w[i]));
+      asm volatile("" : "+v"(b.zraw[i]));
+    }
+  };
+  auto stage = [&](int s, auto cur_c) __attribute__((always_inline)) {
+    constexpr int cur = decltype(cur_c)::value;
+    settle(wb[cur]);
+    if (s + 1 < S) {
+      copy_a(s + 1, (s + 1) & 1);
+      load_w(s + 1, wb[cur ^ 1]);
+      load_scales(s + 1, sc);
+    }
+    compute(s, wb[cur]);
+    if (s + 1 < S) {
+      wait_vm<0>();
+      park_scales((s + 1) & 1, sc);
+    }
+    wait_vm_barrier<0>();  // stage s + 1 landed everywhere; slot s & 1 free
+  };
+  int s = 0;
+  for (; s + 1 < S; s += 2) {
+    stage(s, std::integral_constant<int, 0>{});
+    stage(s + 1, std::integral_constant<int, 1>{});
+  }
+  if (s < S) stage(s, std::integral_constant<int, 0>{});
+
+  // ---- output: row m0 + 16 b + c16, columns n0 + 16 wave + 4 kg + r. The
+  // row scales and the bias are loaded before the first store.
+  const int col0 = n0 + 16 * wave + 4 * kg;
+  const bool vec = (p.N % 4) == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+  float sa[8];
+  float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (!INTEGER) {
+    static_for<0, 8>([&](auto b) { sa[b] = p.a_scale[min(m0 + 16 * decltype(b)::value + c16, p.M - 1)]; });
+    uint32_t braw[4] = {};
+    if (p.bias != nullptr) {
+      if (p.bias_dtype == QG_F32)
+        static_for<0, 4>([&](auto r) { braw[r] = static_cast<const uint32_t*>(p.bias)[min(col0 + decltype(r)::value, p.N - 1)]; });
+      else
+        static_for<0, 4>([&](auto r) {
+          braw[r] = static_cast<const uint16_t*>(p.bias)[min(col0 + decltype(r)::value, p.N - 1)];
+        });
+    }
+    static_for<0, 4>([&](auto r) {
+      const uint32_t x = braw[r];
+      bv[r] = p.bias_dtype == QG_F32   ? __uint_as_float(x)
+              : p.bias_dtype == QG_F16 ? f16_to_f32(static_cast<uint16_t>(x))
+                                       : bf16_to_f32(static_cast<uint16_t>(x));
+    });
+  }
+  const bool has_bias = p.bias != nullptr;
+  static_for<0, 8>([&](auto b_c) {
+    constexpr int b = decltype(b_c)::value;
+    const int row = m0 + 16 * b + c16;
+    if (row >= p.M) return;
+    uint32_t bits[4];
+    static_for<0, 4>([&](auto r_c) {
+      constexpr int r = decltype(r_c)::value;
+      if constexpr (INTEGER) {
+        bits[r] = static_cast<uint32_t>(itot[b][r]);
+      } else {
+        float y = tot[b][r] * sa[b];
+        if (has_bias) y = y + bv[r];
+        bits[r] = __float_as_uint(y);
+      }
+    });
+    uint32_t* orow = static_cast<uint32_t*>(p.out) + static_cast<int64_t>(row) * p.N;
+    if (vec && col0 + 4 <= p.N) {
+      *reinterpret_cast<i32x4*>(orow + col0) = i32x4{static_cast<int>(bits[0]), static_cast<int>(bits[1]),
+                                                     static_cast<int>(bits[2]), static_cast<int>(bits[3])};
+    } else {
+      static_for<0, 4>([&](auto r_c) {
+        constexpr int r = decltype(r_c)::value;
+        if (col0 + r < p.N) orow[col0 + r] = bits[r];
+      });
+    }
+  });
+}
+
 // 4 waves (two workgroups per CU): 8 waves on 128 x 256 tiles halve the A
 // bytes per MAC but took 187 us against 145 us on (4096, 3072, 3072) g128 and
 // 105 against 82 us on (1061, 3072, 3072) g32 (one workgroup per CU: the
@@ -503,8 +782,36 @@ hipError_t launch_g(const W4A8Args& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+constexpr int kN16Waves = 4;
+
+template <int G>
+hipError_t launch_n16(const W4A8Args& p, hipStream_t stream) {
+  constexpr int NW = kN16Waves;
+  const int blocks = ceil_div(p.M, kBM) * ceil_div(p.N, 16 * NW);
+  const dim3 grid(blocks), block(64 * NW);
+  if (p.integer) hipLaunchKernelGGL((k_w4a8_n16<G, true, NW>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((k_w4a8_n16<G, false, NW>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+// The 16-column form where the 4-wave grid leaves the CUs short of waves: at
+// most 128 of its 128 x 128 tiles, or at most 256 with g32, whose four folds
+// per stage make the vector ALU the bound (one MI355X, both kernels in one
+// run: M 512 x N 3072 x K 3072 all groups 15-28 % faster, M 1061 g32 8-13 %;
+// M 1061 g64 / g128, M 2048, M 4096 and N 9216 slower).
+bool use_n16(const W4A8Args& p) {
+  if (p.w8 != nullptr || p.K <= 0 || p.K % kStage != 0) return false;
+  const int64_t tiles = static_cast<int64_t>(ceil_div(p.M, kBM)) * ceil_div(p.N, W8Geo<kW4A8Waves>::BN);
+  return tiles <= 128 || (tiles <= 256 && p.group == 32);
+}
+
 template <bool PREP>
 hipError_t launch_p(const W4A8Args& p, hipStream_t stream) {
+  if (!PREP && use_n16(p)) {
+    if (p.group == 32) return launch_n16<32>(p, stream);
+    if (p.group == 64) return launch_n16<64>(p, stream);
+    return launch_n16<128>(p, stream);
+  }
   if (p.group == 32) return launch_g<32, PREP>(p, stream);
   if (p.group == 64) return launch_g<64, PREP>(p, stream);
   return launch_g<128, PREP>(p, stream);

@@ -476,5 +476,11 @@ def int4_linear_a8(a, p, a_scale, *, bias=None, method="dot4", tile=(64, 64), nu
             _lib.DTYPE_CODE[b.dtype] if b is not None else 0, _lib.ptr(out), int(integer), _lib.stream_of(av)),
             "qg_w4a8_gemm")
     if return_kernel:
-        return out, _lib.kernel_metadata("w4a8_mfma_i32_32x32x32_i8", (128, 128), "k_w4a8")
+        # the library's choice (csrc/w4a8_gemm.hip, use_n16): 16-column waves
+        # for packed weights, K a multiple of 128 and a grid of at most 128
+        # tiles of 128 x 128 (256 at g32)
+        tiles = -(-m // 128) * -(-p.n // 128)
+        if w8 is None and k % 128 == 0 and (tiles <= 128 or (tiles <= 256 and p.group_size == 32)):
+            return out, _lib.kernel_metadata("w4a8_mfma_i32_16x16x32_i8", (128, 64), "k_w4a8_n16")
+        return out, _lib.kernel_metadata("w4a8_mfma_i32_32x32x32_i8", (128, 128), "6k_w4a8I")
     return out

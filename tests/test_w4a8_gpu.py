@@ -76,8 +76,9 @@ def test_w4a8_formats(cuda, g, sym, layout, order):
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 def test_w4a8_shapes_and_tails(cuda, m, n, k, g, layout):
     """Row / column tails, a single row, K = 96, 160, 192, 320, 352, 640 (last
-    stage of 128 K filled by 1, 2 or 3 of its 4 k-steps, or whole); nk words
-    take the kernel's 16-byte weight loads, kn words 4-byte loads."""
+    stage of 128 K filled by 1, 2 or 3 of its 4 k-steps, or whole): K a
+    multiple of 128 takes the 16-column form (these grids are small), other K
+    the 32-column guarded body (nk words as 16-byte loads, kn as 4-byte)."""
     case(f"w4a8 shape {m}x{n}x{k} g{g} {layout}")
     p, c, s, a, sa, bias = make(cuda, m, n, k, g, layout=layout, seed=m + n)
     check(cuda, p, c, s, a, sa, bias, g, f"{m}x{n}x{k}")
@@ -140,6 +141,25 @@ def test_w4a8_extreme_values(cuda):
     assert np.array_equal(_np(y).astype(np.int64), ref_i)
     yf = run(cuda, p, a, sa, bias)
     assert np.array_equal(_np(yf).view(np.uint32), o4.w4a8_linear(a, c, s, sa, 32, bias).view(np.uint32))
+
+
+@pytest.mark.parametrize("m,n,k,g,layout,form", [
+    (300, 2100, 256, 128, "nk", "k_w4a8_n16"),   # 51 tiles: 16-column waves
+    (1100, 2200, 256, 32, "kn", "k_w4a8_n16"),   # 162 tiles at g32: 16-column waves
+    (2048, 1152, 256, 128, "nk", "6k_w4a8I"),    # 144 tiles: 32-column waves, full-K body
+    (1100, 2200, 384, 64, "kn", "6k_w4a8I"),     # 162 tiles at g64: 32-column waves, full-K body
+    (1100, 2200, 320, 64, "nk", "6k_w4a8I"),     # K not a multiple of 128: guarded body
+])
+def test_w4a8_kernel_forms(cuda, m, n, k, g, layout, form):
+    """Every kernel form the library chooses by grid size, group and K,
+    byte-equal to the oracle (integer and float, ragged M and N)."""
+    case(f"w4a8 form {form} {m}x{n}x{k} g{g} {layout}")
+    p, c, s, a, sa, bias = make(cuda, m, n, k, g, layout=layout, seed=m + n + k)
+    y, meta = run(cuda, p, a, sa, bias, return_kernel=True)
+    assert form in (meta["symbol"] or ""), meta
+    assert np.array_equal(_np(y).view(np.uint32), o4.w4a8_linear(a, c, s, sa, g, bias).view(np.uint32))
+    yi = run(cuda, p, a, sa, integer=True)
+    assert np.array_equal(_np(yi).astype(np.int64), o4.w4a8_integer(a, c))
 
 
 def test_w4a8_argument_checks(cuda):

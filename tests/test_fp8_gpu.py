@@ -229,9 +229,7 @@ def test_fused_wide_tiles_ragged(cuda, e5):
 def test_cfg3_full_size(cuda, n):
     """BASELINE configuration 3 at its real shape: M 4096, K 3072, e4m3
     weights with per-channel absmax / 448 scales, bf16 activations and output.
-    512 rows spread over M are checked against the oracle on the CPU, and
-    every output against the oracle's formula evaluated in float64 on the
-    GPU (same bars)."""
+    Every output (4096 x n) is checked against the oracle on the CPU."""
     case(f"cfg3 fp8 m4096 k3072 n{n}")
     g = torch.Generator().manual_seed(3)
     wf = torch.randn(n, 3072, generator=g) * 0.02
@@ -247,22 +245,10 @@ def test_cfg3_full_size(cuda, n):
     w = codes_tensor(codes, False, cuda)
     y = mod().fp8_weight_gemm(a.to(cuda), w, method="fused_dot2", w_scale=torch.from_numpy(s).to(cuda))
     assert torch.isfinite(y).all()
-    rows = np.linspace(0, 4095, 512).astype(int)
-    av = a.float().numpy().astype(np.float64)[rows]
+    av = a.float().numpy().astype(np.float64)
     y64 = o8.fp8_linear(av, codes, s)
     absdot = o8.fp8_linear(np.abs(av), codes & 0x7F, s)
-    check(y[torch.from_numpy(rows).to(cuda)], y64, absdot, torch.bfloat16, f"cfg3 n{n}")
-    # every output: the oracle's formula, float64 (a @ decode(w)^T) * s, evaluated on the GPU
-    a64 = a.to(cuda).double()
-    w64 = torch.from_numpy(o8.decode_bits(codes, False).astype(np.float64)).to(cuda)
-    s64 = torch.from_numpy(s.astype(np.float64)).to(cuda)
-    y_all = (a64 @ w64.T) * s64
-    absdot_all = (a64.abs() @ w64.abs().T) * s64
-    err = (y.double() - y_all).abs()
-    rms = y_all.pow(2).mean().sqrt()
-    assert bool((err <= 1e-2 * rms + 2.0 ** -8 * y_all.abs() * 1.0001 + 1e-30).all()), "cfg3 all rows: BASELINE bar"
-    bound = 2.0 ** -8 * y_all.abs() * 1.0001 + 2.0 ** -20 * absdot_all + 2.0 ** -24
-    assert int((err > bound).sum()) == 0, "cfg3 all rows: beyond one rounding"
+    check(y, y64, absdot, torch.bfloat16, f"cfg3 n{n}")
 
 
 def test_fused_metadata_names_the_launched_tile(cuda):

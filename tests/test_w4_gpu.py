@@ -364,11 +364,10 @@ def test_cfg2_prefill_full_size(cuda):
     """BASELINE configuration 2, prefill M = 2048 at its real shape. This grid
     takes the dequant path (W dequantised once to bf16 in the workspace, the
     reference's dequant formulation, then the 2-byte ping-pong GEMM). Every
-    output is finite; 256 rows spread over M meet the BASELINE bar against the
-    exact float64 product, and match the float64 product of the bf16-rounded
-    weights the GEMM multiplies within one output rounding plus fp32
-    accumulation slack (oracle on the CPU); every output meets the same two
-    bars against those products evaluated in float64 on the GPU."""
+    output is finite, meets the BASELINE bar against the exact float64
+    product of the oracle on the CPU, and matches the float64 product of the
+    bf16-rounded weights the GEMM multiplies within one output rounding plus
+    fp32 accumulation slack (all 2048 x 14336 outputs)."""
     from oracle.int8 import round_to
     case("cfg2 w4a16 m2048 k4096 n14336")
     g = torch.Generator().manual_seed(2)
@@ -379,32 +378,19 @@ def test_cfg2_prefill_full_size(cuda):
     y, md = w4().int4_linear_a16(a.to(cuda), p, method="dot2", return_kernel=True)
     assert md["variant"] == "w4a16_dequant_pingpong"
     assert torch.isfinite(y).all()
-    rows = np.linspace(0, 2047, 256).astype(int)
-    av = act_values(a)[rows]
-    got = y[torch.from_numpy(rows).to(cuda)].float().cpu().numpy().astype(np.float64)
+    av = act_values(a)
+    got = y.float().cpu().numpy().astype(np.float64)
     cen = o4.dequant_baseline(r, floating=False)
     s = bf16_bits_to_f32(r["scales"])
     y64 = o4.w4a16_linear(av, cen, s, 128)
     rms = float(np.sqrt(np.mean(y64 ** 2)))
     assert (np.abs(got - y64) <= 1e-2 * rms + 2.0 ** -8 * np.abs(y64) * 1.0001).all(), "BASELINE bar"
+    del y64
     wq = round_to(o4.dequant_baseline(r), "bf16").astype(np.float64)
     yq = av @ wq.T
     slack = 2.0 ** -17 * (np.abs(av) @ np.abs(wq).T)
     bad = np.abs(got - yq) > 2.0 ** -8 * np.abs(yq) * 1.0001 + slack
     assert not bad.any(), f"{bad.sum()} outputs beyond one rounding of the bf16-weight product"
-    # every output: the same two bars with the products evaluated in float64 on the GPU
-    a64 = a.to(cuda).double()
-    wx = torch.from_numpy((cen.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1))).to(cuda)
-    y_all = a64 @ wx.T
-    err = (y.double() - y_all).abs()
-    rms = y_all.pow(2).mean().sqrt()
-    assert bool((err <= 1e-2 * rms + 2.0 ** -8 * y_all.abs() * 1.0001).all()), "all rows: BASELINE bar"
-    del wx, y_all, err
-    wq64 = torch.from_numpy(wq).to(cuda)
-    yq_all = a64 @ wq64.T
-    slack_all = 2.0 ** -17 * (a64.abs() @ wq64.abs().T)
-    bad_all = (y.double() - yq_all).abs() > 2.0 ** -8 * yq_all.abs() * 1.0001 + slack_all
-    assert int(bad_all.sum()) == 0, "all rows: beyond one rounding of the bf16-weight product"
 
 
 @pytest.mark.parametrize("adtype,layout,group,m,n", [
@@ -419,7 +405,7 @@ def test_w4a16_dequant_path_ragged(cuda, adtype, layout, group, m, n):
     rows) that writes at the output's full row stride. The weights are
     dequantised to the activation dtype, so the result matches the float64
     product of those rounded weights within fp32 accumulation slack, and the
-    exact product within the BASELINE bar; the sampled rows cover both parts."""
+    exact product within the BASELINE bar (every output, both parts)."""
     from oracle.int8 import round_to
     case(f"w4a16 dequant path m{m} n{n} k512 {adtype} {layout} g{group}")
     k = 512
@@ -431,8 +417,7 @@ def test_w4a16_dequant_path_ragged(cuda, adtype, layout, group, m, n):
     y, md = w4().int4_linear_a16(a.to(cuda), p, bias=b.to(cuda), method="dot2", return_kernel=True)
     assert md["variant"] == "w4a16_dequant_pingpong"
     y32 = w4().w4a16_gemm(a.to(cuda), p, b.to(cuda), out_dtype=torch.float32)
-    rows = np.linspace(0, m - 1, 128).astype(int)
-    av = act_values(a)[rows]
+    av = act_values(a)
     # the weights the GEMM multiplies: the library's own dequantisation (checked
     # bit-exact against the oracle by the unpack tests), in the activation dtype
     wq = w4().unpack_int4(p, dtype=adtype).float().cpu().numpy().astype(np.float64)
@@ -440,12 +425,12 @@ def test_w4a16_dequant_path_ragged(cuda, adtype, layout, group, m, n):
     bias64 = act_values(b)
     yq = av @ wq.T + bias64
     yx = av @ wexact.T + bias64
-    got32 = y32[torch.from_numpy(rows).to(cuda)].cpu().numpy().astype(np.float64)
+    got32 = y32.cpu().numpy().astype(np.float64)
     slack = 2.0 ** -17 * (np.abs(av) @ np.abs(wq).T + np.abs(bias64))
     assert (np.abs(got32 - yq) <= slack).all(), "fp32 output vs rounded-weight product"
     rms = float(np.sqrt(np.mean(yx ** 2)))
     half = 2.0 ** -11 if adtype == torch.float16 else 2.0 ** -8
-    got = y[torch.from_numpy(rows).to(cuda)].float().cpu().numpy().astype(np.float64)
+    got = y.float().cpu().numpy().astype(np.float64)
     assert (np.abs(got - yx) <= 1e-2 * rms + half * np.abs(yx) * 1.0001).all(), "BASELINE bar"
 
 

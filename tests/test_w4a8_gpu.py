@@ -86,15 +86,14 @@ def test_w4a8_shapes_and_tails(cuda, m, n, k, g, layout):
 
 def test_w4a8_reference_check_shapes(cuda):
     """The reference's own check (bench_int4_v07.py:149-171): g32 affine, kn,
-    low order, bias, methods dot4 / dot8 / dot4_words, byte-equal; the
-    1061 x 3072 x 3072 case on a sample of rows."""
+    low order, bias, methods dot4 / dot8 / dot4_words, byte-equal on every
+    output, the 1061 x 3072 x 3072 case included."""
     for m, n, k in ((37, 53, 384), (19, 3072, 3072), (1061, 3072, 3072)):
         case(f"w4a8 reference check {m}x{n}x{k}")
         p, c, s, a, sa, bias = make(cuda, m, n, k, 32, layout="kn", seed=20261107)
-        rows = np.arange(m) if m < 100 else np.linspace(0, m - 1, 48).astype(int)
-        ref = o4.w4a8_linear(a[rows], c, s, sa[rows], 32, bias)
+        ref = o4.w4a8_linear(a, c, s, sa, 32, bias)
         for method in ("dot4", "dot8", "dot4_words"):
-            y = _np(run(cuda, p, a, sa, bias, method=method))[rows]
+            y = _np(run(cuda, p, a, sa, bias, method=method))
             assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), (m, n, k, method)
 
 

@@ -161,6 +161,26 @@ def test_w4a8_kernel_forms(cuda, m, n, k, g, layout, form):
     assert np.array_equal(_np(yi).astype(np.int64), o4.w4a8_integer(a, c))
 
 
+def test_w4a8_random_shapes(cuda):
+    """24 seeded random cases over M, N, K (K a multiple of 128 or not), group
+    size, word layout, nibble order and symmetric / affine packing: integer
+    and float outputs byte-equal to the oracle, whichever form the grid takes."""
+    rng = np.random.default_rng(20261202)
+    for i in range(24):
+        g = int(rng.choice(o4.GROUPS))
+        k = g * int(rng.integers(1, 1536 // g + 1))
+        m, n = int(rng.integers(1, 700)), int(rng.integers(1, 900))
+        layout = str(rng.choice(["nk", "kn"]))
+        order = str(rng.choice(["low", "high"]))
+        sym = bool(rng.integers(0, 2))
+        case(f"w4a8 random {i}: {m}x{n}x{k} g{g} {layout} {order} sym={sym}")
+        p, c, s, a, sa, bias = make(cuda, m, n, k, g, sym, layout, order, seed=1000 + i)
+        yf = run(cuda, p, a, sa, bias)
+        assert np.array_equal(_np(yf).view(np.uint32), o4.w4a8_linear(a, c, s, sa, g, bias).view(np.uint32)), i
+        yi = run(cuda, p, a, sa, integer=True)
+        assert np.array_equal(_np(yi).astype(np.int64), o4.w4a8_integer(a, c)), i
+
+
 def test_w4a8_argument_checks(cuda):
     case("w4a8 argument checks")
     p, c, s, a, sa, bias = make(cuda, 8, 64, 256, 32)

@@ -474,7 +474,7 @@ def run_moe(torch, dev, iters=20):
 
 
 def run_w4a8(torch, dev, iters=20):
-    """Secondary (SURVEY next row, no BASELINE config): W4A8 on the int8 MFMA,
+    """Secondary (no BASELINE configuration): W4A8 on the int8 MFMA,
     int4_linear_a8 float output, on the cfg0 shape with g128 affine nk
     weights and on the reference's own check shape (M 1061, g32, kn).
     TOPS = 2 M N K per call; HIP events over `iters` back-to-back calls."""
@@ -502,8 +502,9 @@ def run_w4a8(torch, dev, iters=20):
             samples.append(e0.elapsed_time(e1) / iters)
         us = statistics.median(samples) * 1e3
         tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+        _, md = w4.int4_linear_a8(a, p, sa, return_kernel=True)
         res[label] = {"us": round(us, 1), "TOPS": round(tops, 1), "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4),
-                      "shape": [m, n, k], "group": g}
+                      "shape": [m, n, k], "group": g, "kernel": md["variant"], "tile": md["tile"]}
     return res
 
 
@@ -793,8 +794,8 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(run with --gpus 1; sharding is described in DESIGN.md)", file=sys.stderr, flush=True)
+        print("bench.py measures one GPU only: this build has no multi-GPU path; run with --gpus 1",
+              file=sys.stderr, flush=True)
         sys.exit(2)
     if args.rounds < 1:
         print("--rounds must be at least 1", file=sys.stderr, flush=True)

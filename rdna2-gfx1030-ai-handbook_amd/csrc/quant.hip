@@ -342,7 +342,9 @@ __global__ __launch_bounds__(512) void k_rot_quant_rows_reg(const char* x, int64
 }
 
 // The register form's contract (K % 512 == 0, groups 8 .. 512, 16-byte
-// aligned rows); its slot count per lane.
+// aligned rows); its slot count per lane (at most 4: the launcher's largest
+// instantiation).
+static_assert(QG_ROT_MAX_K <= 4 * 512 * 8, "register ConvRot form: at most 4 slots of 8 values per lane");
 inline int rot_reg_slots(const void* x, int x_dtype, int64_t x_sm, int64_t K, int G, int8_t* q, int64_t q_sm) {
   const int es = x_dtype == QG_F32 ? 4 : 2;
   if (K % 512 != 0 || K > QG_ROT_MAX_K || G < 8 || G > 512) return 0;

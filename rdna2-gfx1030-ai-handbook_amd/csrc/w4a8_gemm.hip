@@ -368,7 +368,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_w4a8(W4A8Args p) {
 
   // ---- pipeline: stage s + 1's copies and loads are issued before stage s
   // computes; one barrier per stage.
-  WStage<PREP> wb[2];
+  WStage<PREP> wb[2] = {};  // zero: the settle step touches every zero-point slot
   uint32_t sc[2] = {0u, 0u};
   copy_a(0, 0);
   load_w(0, wb[0]);
@@ -658,7 +658,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_w4a8_n16(W4A8Args 
   // ---- pipeline: stage s + 1's copies and loads are issued before stage s
   // computes (this stage's registers touched first, see k_w4a8); one barrier
   // per stage
-  Stage wb[2];
+  Stage wb[2] = {};  // zero: the settle step touches every zero-point slot
   uint32_t sc = 0u;
   copy_a(0, 0);
   load_w(0, wb[0]);

@@ -416,7 +416,8 @@ int qg_moe_dispatch_qx(const float* logits, int64_t l_sm, int64_t tokens, int n_
  * tokens * top_k for QG_MOE_EPI_ROUTE) of row stride out_sm (elements). Tile
  * entries naming an expert >= n_experts or rows outside [0, rows_max) are
  * skipped, row_token entries are clamped into [0, a_rows) and route rows
- * outside [0, out_rows) are not written. */
+ * outside [0, out_rows) are not written. At most 131072 work items
+ * (tiles_max * ceil(n / 256)); more return hipErrorInvalidValue. */
 int qg_moe_grouped_gemm(const int8_t* a, int64_t a_sm, int64_t a_rows, const int32_t* row_token,
                         int64_t rows_max, int64_t k, const int8_t* w, int64_t w_sn, int64_t w_estride,
                         int64_t n, int n_experts, const int32_t* tiles, int64_t tiles_max,

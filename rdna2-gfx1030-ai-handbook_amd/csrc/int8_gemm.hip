@@ -1211,6 +1211,11 @@ __device__ __forceinline__ float silu(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
 }
 
+// Candidate work items per workgroup of the grouped kernel: their table
+// entries are copied into LDS at the start (launch_i8_moe_gemm rejects plans
+// that would need more).
+constexpr int kMoeItems = 512;
+
 // Grouped (MoE) INT8 GEMM on the ping-pong main loop, persistent. Work items
 // are the device tile table's tiles in use (tile 0's spare field holds their
 // number) x ceil(N / G::BN) column tiles: tile t = {expert e (< 0: none), first
@@ -1226,22 +1231,40 @@ __device__ __forceinline__ float silu(float g) {
 //                        (in the transposed layout the gate and up values of
 //                        a feature sit in the same lane, registers r and r + 8)
 //   QG_MOE_EPI_ROUTE     out bf16 [slots, N] row row_slot[r] = v * row_weight[r]
-// As in the dense persistent body, the next item's table entry, copy offsets
-// and per-row parameters are read and its stage-0 copies (A slot 0, W slot 0)
-// issued before the current item's epilogue, which stages its bf16 rows 32 at
-// a time in A slots 1-2; a barrier after the epilogue keeps the next item's
-// parked parameters and stage-1 copies off the LDS the epilogue still reads.
-// The staged epilogue's stores are buffer stores whose lanes without a
-// valid target get an offset past the buffer's range, which the hardware
-// drops: every wave issues the same number of them per item, so the next
-// main loop lets them fly past its stage-0 waits (as the dense body does).
+// As in the dense persistent body, the next item's stage-0 copies (A slot 0,
+// W slot 0) are issued before the current item's epilogue, which stages its
+// bf16 rows 32 at a time in A slots 1-2, and a barrier after the epilogue
+// keeps the next item's stage-1 copies off the LDS the epilogue still reads.
+// The staged epilogue's stores are buffer stores whose lanes without a valid
+// target get an offset past the buffer's range, which the hardware drops:
+// every wave issues the same number of them per item, so the next main loop
+// lets them fly past its stage-0 waits.
+// No item-boundary step waits for memory: the table entries of a workgroup's
+// candidate items are copied into LDS at the start; the row_token values of
+// item i + 1's rows are copied into LDS at item i - 1's prefetch point (after
+// its main loop) and read at item i's, where they give item i + 1's A copy
+// offsets and the copies of its epilogue parameters (row scale, routing
+// weight, output row, column scale) straight into LDS (token and parameter
+// buffers alternate by item parity). Every such copy lands before the next
+// main loop's first barrier (the X waves wait for all their copies at each
+// stage). No register loaded from memory is read after the epilogue's
+// stores are issued: the compiler's own wait for it would drain the stores.
 template <typename G, int MOE>
 __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
 #pragma clang fp contract(off)
   constexpr int YS = pp_copies<G>();
+  constexpr int YA = G::BM / 32;                                    // A copies per Y wave and stage
   constexpr int EPI_BASE = G::STAGE_A;                              // A slots 1-2
   constexpr int EPI_REGION = (G::NA - 1) * G::STAGE_A / G::NW;     // bytes per wave
-  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES + 8 * G::BM];
+  // parameter buffer: row scales, routing weights, output rows, column scales
+  constexpr int P_SA = 0, P_RW = 4 * G::BM, P_DST = 8 * G::BM, P_SB = 12 * G::BM;
+  constexpr int PSZ = 12 * G::BM + 4 * G::BN;
+  constexpr int TAB = G::RING + 2 * PSZ;    // candidate table, kMoeItems x {e, m0, m_end, n0}
+  constexpr int TOK = TAB + 16 * kMoeItems;  // two token buffers of BM rows
+  __shared__ __attribute__((aligned(1024))) char smem[TOK + 8 * G::BM];
+  static_assert(TOK + 8 * G::BM <= 160 * 1024, "LDS per CU");
+  static_assert(G::BM % 64 == 0 && G::BN % 64 == 0 && G::BM <= 256 && G::BN <= 256,
+                "parameter copies: whole waves of the first four");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1256,66 +1279,95 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
   const int first = (static_cast<int>(blockIdx.x) & 7) * per_xcd;
   const int last = min(first + per_xcd, used);
   const int S = p.K / G::KS;
+  const int item0 = first + (static_cast<int>(blockIdx.x) >> 3);
+  const int nitems = item0 < last ? min(ceil_div(last - item0, slots), kMoeItems) : 0;
 
-  // Tile of work item w; false when its table entry names no tile, or a tile
-  // outside the operands (the item is skipped by the whole workgroup).
-  auto tile_of = [&](int w, int& e, int& m0, int& m_end, int& n0) -> bool {
+  // candidate c = item item0 + c slots: {e, m0, m_end, n0}, e = -1 where its
+  // table entry names no tile or a tile outside the operands
+  i32x4* const tab = reinterpret_cast<i32x4*>(smem + TAB);
+  for (int c = tid; c < nitems; c += G::THREADS) {
+    const int w = item0 + c * slots;
     const int tile = w / ncol, ct = w - tile * ncol;
-    e = p.tiles[4 * tile];
-    m0 = p.tiles[4 * tile + 1];
-    m_end = p.tiles[4 * tile + 2];
-    n0 = ct * G::BN;
-    return e >= 0 && e < p.n_experts && m0 >= 0 && m0 < p.M && m_end > m0 && m_end <= p.M;
+    const int e_ = p.tiles[4 * tile], m0_ = p.tiles[4 * tile + 1], mend_ = p.tiles[4 * tile + 2];
+    const bool ok = e_ >= 0 && e_ < p.n_experts && m0_ >= 0 && m0_ < p.M && mend_ > m0_ && mend_ <= p.M;
+    tab[c] = i32x4{ok ? e_ : -1, m0_, mend_, ct * G::BN};
+  }
+  __syncthreads();
+  auto next_valid = [&](int c) {
+    while (c < nitems && __builtin_amdgcn_readfirstlane(tab[c][0]) < 0) ++c;
+    return c;
   };
+  auto entry = [&](int c, int& e_, int& m0_, int& mend_, int& n0_) {
+    const i32x4 t = tab[c];
+    e_ = __builtin_amdgcn_readfirstlane(t[0]);
+    m0_ = __builtin_amdgcn_readfirstlane(t[1]);
+    mend_ = __builtin_amdgcn_readfirstlane(t[2]);
+    n0_ = __builtin_amdgcn_readfirstlane(t[3]);
+  };
+  int cur = next_valid(0);
+  if (cur >= nitems) return;
   int e = 0, m0 = 0, m_end = 0, n0 = 0;
-  int item = first + (static_cast<int>(blockIdx.x) >> 3);
-  while (item < last && !tile_of(item, e, m0, m_end, n0)) item += slots;
-  if (item >= last) return;
+  entry(cur, e, m0, m_end, n0);
+  int nxt = next_valid(cur + 1);
+  int e1 = 0, m1 = 0, mend1 = 0, n1 = 0;
+  if (nxt < nitems) entry(nxt, e1, m1, mend1, n1);
 
-  // per-row / per-column parameters of a tile (rows clamped into the
-  // routed-row arrays), held in registers until the tile's main loop parks them
-  float ld_sa = 0.0f, ld_sb = 0.0f, ld_rw = 0.0f;
-  int ld_dst = -1;
-  auto fetch_params = [&](int e_, int m0_, int n0_) __attribute__((always_inline)) {
-    if (tid < G::BM) {
-      const int r = min(m0_ + tid, p.M - 1);
-      const int src = p.row_token ? min(max(p.row_token[r], 0), p.a_rows - 1) : min(r, p.a_rows - 1);
-      if constexpr (MOE != QG_MOE_EPI_I32) ld_sa = p.a_scale[src];
-      if constexpr (MOE == QG_MOE_EPI_ROUTE) {
-        ld_rw = p.row_weight[r];
-        ld_dst = p.row_slot[r];
-      }
-    }
-    if constexpr (MOE != QG_MOE_EPI_I32) {
-      if (tid < G::BN) ld_sb = p.b_scale[static_cast<int64_t>(e_) * p.N + min(n0_ + tid, p.N - 1)];
-    }
+  // row_token values of an item's rows (entry j: row min(m0 + j, M - 1)),
+  // copied into token buffer `buf` by the X waves (each 64 rows)
+  auto copy_tokens = [&](int m0_, int buf) __attribute__((always_inline)) {
+    if (p.row_token == nullptr || !grp_x || 64 * wave >= G::BM) return;
+    dma4s(p.row_token, 4u * static_cast<uint32_t>(min(m0_ + 64 * wave + lane, p.M - 1)),
+          lds_addr_of(smem + TOK + buf * 4 * G::BM) + 256 * wave);
+  };
+  // A row of routed row m0_ + j (j < BM; the row clamped to M - 1)
+  auto src_row = [&](int m0_, int j, int buf) {
+    const int r = min(m0_ + j, p.M - 1);
+    if (p.row_token == nullptr) return min(r, p.a_rows - 1);
+    const int tok = reinterpret_cast<const int*>(smem + TOK + buf * 4 * G::BM)[r - m0_];
+    return min(max(tok, 0), p.a_rows - 1);
   };
   uint32_t voff[YS];
-  auto plan_offsets = [&](int m0_, int n0_) __attribute__((always_inline)) {
+  auto plan_offsets = [&](int m0_, int n0_, int buf) __attribute__((always_inline)) {
     const CopyPlan<4> plan(grp_x ? n0_ : m0_, wave & 3, lane);
     static_for<0, YS>([&](auto i_c) {
       constexpr int I = decltype(i_c)::value;
       if (grp_x) {
         voff[I] = static_cast<uint32_t>(min(plan.row0 + 32 * I, p.N - 1)) * static_cast<uint32_t>(p.w_sn) +
                   plan.chunk16;
-      } else {
-        const int r = min(plan.row0 + 32 * I, p.M - 1);
-        const int src = p.row_token ? min(max(p.row_token[r], 0), p.a_rows - 1) : min(r, p.a_rows - 1);
+      } else if constexpr (I < YA) {
+        const int src = src_row(m0_, plan.row0 - m0_ + 32 * I, buf);
         voff[I] = static_cast<uint32_t>(src) * static_cast<uint32_t>(p.a_sm) + plan.chunk16;
       }
     });
   };
+  // epilogue parameters of an item, copied into parameter buffer `buf` by the
+  // X waves (each 64 rows / columns)
+  auto copy_params = [&](int e_, int m0_, int n0_, int buf) __attribute__((always_inline)) {
+    if constexpr (MOE != QG_MOE_EPI_I32) {
+      if (!grp_x) return;
+      const uint32_t pb = lds_addr_of(smem + G::RING + buf * PSZ) + 256 * wave;
+      if (64 * wave < G::BM) {
+        const int r = min(m0_ + 64 * wave + lane, p.M - 1);
+        dma4s(p.a_scale, 4u * static_cast<uint32_t>(src_row(m0_, 64 * wave + lane, buf)), pb + P_SA);
+        if constexpr (MOE == QG_MOE_EPI_ROUTE) {
+          dma4s(p.row_weight, 4u * static_cast<uint32_t>(r), pb + P_RW);
+          dma4s(p.row_slot, 4u * static_cast<uint32_t>(r), pb + P_DST);
+        }
+      }
+      if (64 * wave < G::BN)
+        dma4s(p.b_scale + static_cast<int64_t>(e_) * p.N,
+              4u * static_cast<uint32_t>(min(n0_ + 64 * wave + lane, p.N - 1)), pb + P_SB);
+    }
+  };
   const char* a_base = reinterpret_cast<const char*>(p.a);
   auto w_base = [&](int e_) { return reinterpret_cast<const char*>(p.w) + static_cast<int64_t>(e_) * p.w_estride; };
-  fetch_params(e, m0, n0);
-  plan_offsets(m0, n0);
-
-  // row scales, column scales, row weights and output rows (the latter two
-  // after the GEMM's own parameter area)
-  float* sa_lds = reinterpret_cast<float*>(smem + G::SC_A);
-  float* sb_lds = reinterpret_cast<float*>(smem + G::SC_B);
-  float* rw_lds = reinterpret_cast<float*>(smem + G::LDS_BYTES);
-  int* dst_lds = reinterpret_cast<int*>(smem + G::LDS_BYTES + G::BM * 4);
+  // tokens of the first two items, then the first item's offsets and parameters
+  copy_tokens(m0, 0);
+  if (nxt < nitems) copy_tokens(m1, 1);
+  wait_vm<0>();
+  __syncthreads();
+  plan_offsets(m0, n0, 0);
+  copy_params(e, m0, n0, 0);
 
   // bf16 outputs whose rows take whole 16-byte chunks are staged per wave, 32
   // rows at a time, and written as row chunks; int32 (test) output goes
@@ -1329,7 +1381,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
   const int out_cols = MOE == QG_MOE_EPI_SILU_MUL ? p.N / 2 : p.N;
   // ST: the staged epilogue's 16-byte stores per wave and item
   constexpr int ST = STAGED ? G::FM * (32 * CH / 64) : 0;
-  static_assert(ST + YS < 64, "vmcnt range");
+  static_assert(ST + YS + 4 < 64, "vmcnt range");
   const int64_t out_bytes = static_cast<int64_t>(p.out_rows) * p.out_sm * 2;
   const bool staged = STAGED && (out_cols % 8) == 0 && (p.out_sm % 8) == 0 &&
                       (reinterpret_cast<uintptr_t>(p.out) & 15) == 0 && out_bytes <= kOobOffset;
@@ -1339,6 +1391,7 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
   char* const region = smem + EPI_BASE + wave * EPI_REGION;
 
   bool pre = false;
+  int buf = 0;
   i32x16 acc[G::FM][G::FN];
   for (;;) {
     // lane-derived offsets recomputed per item instead of hoisted (registers)
@@ -1347,31 +1400,34 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
     static_for<0, G::FM>([&](auto i) {
       static_for<0, G::FN>([&](auto j) { acc[i][j] = i32x16{}; });
     });
+    // the parameter copies complete with the main loop's first waits (issued
+    // before the stage-0 copies); K = 0 has no such wait
     auto park = [&]() __attribute__((always_inline)) {
-      if (tid < G::BM) {
-        sa_lds[tid] = ld_sa;
-        rw_lds[tid] = ld_rw;
-        dst_lds[tid] = ld_dst;
-      }
-      if (tid < G::BN) sb_lds[tid] = ld_sb;
+      if (S <= 0) wait_vm<0>();
     };
     pp_mainloop<G, MfmaI8, ST>(acc, smem, a_base, w_base(e), voff, S, wave, lane_t, pre, park, staged);
 
-    // the next item: its table entry, parameters, copy offsets and stage-0
-    // copies, ahead of this item's epilogue. The parameters come first: their
-    // row gathers wait for loads, which would also wait for copies issued
-    // before them.
-    int nitem = item + slots;
-    int e1 = 0, m1 = 0, mend1 = 0, n1 = 0;
-    while (nitem < last && !tile_of(nitem, e1, m1, mend1, n1)) nitem += slots;
-    const bool more = nitem < last;
+    // the next item: its copy offsets, parameter copies and stage-0 copies
+    // ahead of this item's epilogue, then the tokens of the item after it
+    const bool more = nxt < nitems;
+    int nn = nitems, e2 = 0, m2 = 0, mend2 = 0, n2 = 0;
     if (more) {
-      fetch_params(e1, m1, n1);
-      plan_offsets(m1, n1);
+      plan_offsets(m1, n1, buf ^ 1);
+      copy_params(e1, m1, n1, buf ^ 1);
       if (S > 0) pp_prefetch0<G>(smem, a_base, w_base(e1), voff, wave);
+      nn = next_valid(nxt + 1);
+      if (nn < nitems) {
+        entry(nn, e2, m2, mend2, n2);
+        copy_tokens(m2, buf);  // this item's tokens are no longer read
+      }
     }
 
     // ---- epilogue of this item ----------------------------------------------
+    const char* const pbuf = smem + G::RING + buf * PSZ;
+    const float* sa_lds = reinterpret_cast<const float*>(pbuf + P_SA);
+    const float* rw_lds = reinterpret_cast<const float*>(pbuf + P_RW);
+    const int* dst_lds = reinterpret_cast<const int*>(pbuf + P_DST);
+    const float* sb_lds = reinterpret_cast<const float*>(pbuf + P_SB);
     const int lr = lane_t & 31, lq = 4 * (lane_t >> 5);
     static_for<0, G::FM>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
@@ -1470,11 +1526,17 @@ __global__ __launch_bounds__(G::THREADS, 1) void k_i8_moe_pp(I8GemmArgs p) {
     });
     if (!more) break;
     wait_lds_barrier();
-    item = nitem;
+    cur = nxt;
     e = e1;
     m0 = m1;
     m_end = mend1;
     n0 = n1;
+    nxt = nn;
+    e1 = e2;
+    m1 = m2;
+    mend1 = mend2;
+    n1 = n2;
+    buf ^= 1;
     pre = S > 0;
   }
 }
@@ -1530,6 +1592,9 @@ hipError_t launch_i8_moe_gemm(const I8GemmArgs& p, hipStream_t stream) {
   const long items = static_cast<long>(p.tiles_max) * ceil_div(p.N, G::BN);
   if (items == 0) return hipSuccess;
   const int blocks = items < kPersistentCUs ? static_cast<int>((items + 7) & ~7L) : kPersistentCUs;
+  // candidate items per workgroup: its share of one XCD's contiguous range
+  const long per_xcd = (items + 7) / 8, slots = blocks / 8;
+  if ((per_xcd + slots - 1) / slots > kMoeItems) return hipErrorInvalidValue;
   switch (p.moe_epi) {
     case QG_MOE_EPI_I32:
       hipLaunchKernelGGL((k_i8_moe_pp<G, QG_MOE_EPI_I32>), dim3(blocks), dim3(G::THREADS), 0, stream, p);

@@ -878,18 +878,28 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 // 4 adjacent floats 32 j + 8 g + lq .. + 3 of a per-column LDS vector.
 __device__ __forceinline__ f32x4 col4(const float* v, int c0) { return *reinterpret_cast<const f32x4*>(v + c0); }
 
-// Epilogue of the dense ping-pong kernel (transposed accumulators; row scales,
-// column scales and fp32 bias values parked at SC_A, SC_B and SC_BIAS).
+// Epilogue parameters of the dense ping-pong kernel in LDS: BM row scales,
+// BN column scales, BN bias values (copied as raw words, fp32 bits or fp16 /
+// bf16 bits zero-extended, and widened to fp32 in place before the main loop
+// opens), per parameter buffer.
+template <typename G>
+struct PpParams {
+  static constexpr int SA = 0, SB = 4 * G::BM, BIAS = 4 * G::BM + 4 * G::BN;
+  static constexpr int BYTES = 4 * G::BM + 8 * G::BN;
+};
+
+// Epilogue of the dense ping-pong kernel (transposed accumulators; row
+// scales, column scales and bias words in the parameter buffer at pbuf).
 // Full tiles are staged per wave in its own part of the rings and leave as
 // whole 16-byte row chunks; edge tiles store element-wise.
 template <typename G, int OUT, int MODE, bool RES, int STAGE_BASE = 0, int REGION = G::RING / G::NW,
           bool NT = false, typename ACCV = i32x16>
 __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&acc)[G::FM][G::FN], char* smem,
-                                            int m0, int n0, int wr, int wc, int wave, int lane) {
+                                            const char* pbuf, int m0, int n0, int wr, int wc, int wave, int lane) {
 #pragma clang fp contract(off)
-  const float* sa_lds = reinterpret_cast<const float*>(smem + G::SC_A);
-  const float* sb_lds = reinterpret_cast<const float*>(smem + G::SC_B);
-  const float* bv_lds = reinterpret_cast<const float*>(smem + G::SC_BIAS);
+  const float* sa_lds = reinterpret_cast<const float*>(pbuf + PpParams<G>::SA);
+  const float* sb_lds = reinterpret_cast<const float*>(pbuf + PpParams<G>::SB);
+  const float* bv_lds = reinterpret_cast<const float*>(pbuf + PpParams<G>::BIAS);
   const bool has_bias = p.bias != nullptr;
   const int lr = lane & 31, lq = 4 * (lane >> 5);
   float sa[G::FM];
@@ -1024,7 +1034,12 @@ __device__ __forceinline__ void pp_epilogue(const I8GemmArgs& p, const ACCV (&ac
 // stage-0 copies (A slot 0, W slot 0) are issued before the current tile's
 // epilogue, which stages in A slots 1-2, so the next tile's first copy latency
 // overlaps the epilogue; a barrier after the epilogue keeps the next tile's
-// parked parameters and stage-1 copies off the LDS the epilogue still reads.
+// stage-1 copies off the LDS the epilogue still reads. The epilogue
+// parameters (row scales, column scales, bias words) are copied straight
+// into LDS by the X waves, into one of two parameter buffers (tile parity),
+// with the next tile's stage-0 copies: no register loaded from memory is read
+// after the epilogue's stores are issued, where the compiler's own wait for
+// it would drain those stores before the next main loop.
 // The body is shared by the INT8 kernel (MF = MfmaI8, 1-byte operands) and the
 // 2-byte kernel (MfmaHalf, fp16 / bf16 operands: a 128-byte stage row holds 64
 // K elements, four 32x32x16 k-steps); ES is the operand element size.
@@ -1042,7 +1057,11 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
   constexpr bool PREF = out_size<OUT>() == 2 && 32 * (G::WN * 2 + 16) <= (G::NA - 1) * G::STAGE_A / G::NW;
   constexpr int EPI_BASE = PREF ? G::STAGE_A : 0;
   constexpr int EPI_REGION = PREF ? (G::NA - 1) * G::STAGE_A / G::NW : G::RING / G::NW;
-  __shared__ __attribute__((aligned(1024))) char smem[G::LDS_BYTES];
+  using PP = PpParams<G>;
+  __shared__ __attribute__((aligned(1024))) char smem[G::RING + 2 * PP::BYTES];
+  static_assert(G::RING + 2 * PP::BYTES <= 160 * 1024, "LDS per CU");
+  static_assert(G::BM % 64 == 0 && G::BN % 64 == 0 && G::BM <= 256 && G::BN <= 256,
+                "parameter copies: whole waves of the first four");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1081,11 +1100,40 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     });
   };
 
+  // epilogue parameters of a tile into parameter buffer `buf`: X wave w
+  // copies rows / columns 64 w .. 64 w + 63 (constants where an operand is
+  // absent are written directly)
+  auto copy_params = [&](int m0_, int n0_, int buf) __attribute__((always_inline)) {
+    if constexpr (MODE != EPI_INT) {
+      if (!grp_x) return;
+      char* const pb = smem + G::RING + buf * PP::BYTES;
+      const uint32_t pba = lds_addr_of(pb) + 256 * wave;
+      if (64 * wave < G::BM) {
+        if (p.a_scale)
+          dma4s(p.a_scale, 4u * static_cast<uint32_t>(min(m0_ + 64 * wave + lane, p.M - 1)), pba + PP::SA);
+        else
+          reinterpret_cast<float*>(pb + PP::SA)[64 * wave + lane] = 1.0f;
+      }
+      if (64 * wave < G::BN) {
+        const uint32_t col = static_cast<uint32_t>(min(n0_ + 64 * wave + lane, p.N - 1));
+        if (p.b_scale)
+          dma4s(p.b_scale, p.b_scalar ? 0u : 4u * col, pba + PP::SB);
+        else
+          reinterpret_cast<float*>(pb + PP::SB)[64 * wave + lane] = 1.0f;
+        if (p.bias != nullptr) {  // the epilogue reads the bias words only with a bias
+          if (p.bias_dtype == QG_F32) dma4s(p.bias, 4u * col, pba + PP::BIAS);
+          else dma2s(p.bias, 2u * col, pba + PP::BIAS);
+        }
+      }
+    }
+  };
+
   int t = blockIdx.x;
   int m0, n0;
   tile_origin_at<G::BM, G::BN>(p, t, m0, n0);
-  EpiParams ep = fetch_epi_params<G::BM, G::BN, MODE>(p, m0, n0, tid);
   plan_offsets(m0, n0);
+  copy_params(m0, n0, 0);
+  int buf = 0;
   bool pre = false;
   bool stores_fly = false;
   // lower bound of the full-tile epilogue's 16-byte stores per wave (2-byte
@@ -1110,12 +1158,16 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     static_for<0, G::FM>([&](auto i) {
       static_for<0, G::FN>([&](auto j) { acc[i][j] = typename MF::acc_t{}; });
     });
+    // the parameter copies complete with the main loop's first waits (issued
+    // before the stage-0 copies; K = 0 has no such wait); each X wave then
+    // widens the bias words it copied to fp32 in place
     auto park = [&]() __attribute__((always_inline)) {
+      if (S <= 0) wait_vm<0>();
       if constexpr (MODE != EPI_INT) {
-        if (tid < G::BM) reinterpret_cast<float*>(smem + G::SC_A)[tid] = ep.sa;
-        if (tid < G::BN) {
-          reinterpret_cast<float*>(smem + G::SC_B)[tid] = ep.sb;
-          reinterpret_cast<float*>(smem + G::SC_BIAS)[tid] = bias_value(ep.bias, p.bias_dtype);
+        if (grp_x && 64 * wave < G::BN && p.bias != nullptr && p.bias_dtype != QG_F32) {
+          uint32_t* const bw = reinterpret_cast<uint32_t*>(smem + G::RING + buf * PP::BYTES + PP::BIAS);
+          const uint32_t bits = bw[64 * wave + lane];
+          bw[64 * wave + lane] = __float_as_uint(bias_value(bits, p.bias_dtype));
         }
       }
     };
@@ -1125,11 +1177,10 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     const int tn = t + static_cast<int>(gridDim.x);
     const bool more = tn < total;
     int m1 = 0, n1 = 0;
-    EpiParams ep1;
     if (more) {
       tile_origin_at<G::BM, G::BN>(p, tn, m1, n1);
-      ep1 = fetch_epi_params<G::BM, G::BN, MODE>(p, m1, n1, tid);
       plan_offsets(m1, n1);
+      copy_params(m1, n1, buf ^ 1);
       if (PREF && S > 0) pp_prefetch0<G>(smem, a_base, w_base, voff, wave);
     }
     // the full-tile epilogue of 2-byte outputs issues kStoresPerWave 16-byte
@@ -1137,7 +1188,8 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     // tile's stage-0 copies
     stores_fly = PREF && m0 + G::BM <= p.M && n0 + G::BN <= p.N && ((out_ld(p) * out_size<OUT>()) % 16) == 0 &&
                  (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
-    pp_epilogue<G, OUT, MODE, RES, EPI_BASE, EPI_REGION, ES == 1>(p, acc, smem, m0, n0, wr, wc, wave, lane_t);
+    pp_epilogue<G, OUT, MODE, RES, EPI_BASE, EPI_REGION, ES == 1>(p, acc, smem, smem + G::RING + buf * PP::BYTES,
+                                                                  m0, n0, wr, wc, wave, lane_t);
     if constexpr (STAMP) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       t_epi = static_cast<uint32_t>(__builtin_amdgcn_s_memtime());
@@ -1147,7 +1199,7 @@ __device__ __forceinline__ void pp_gemm_body(const I8GemmArgs& p) {
     t = tn;
     m0 = m1;
     n0 = n1;
-    ep = ep1;
+    buf ^= 1;
     pre = PREF && S > 0;
   }
   if constexpr (STAMP) {

@@ -190,6 +190,21 @@ __device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t
       : "memory");
 }
 
+// 2-byte variant (global_load_lds_ushort): lane i writes the element
+// zero-extended to 32 bits at [lds_addr + 4 i, lds_addr + 4 i + 4).
+__device__ __forceinline__ void dma2s(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_ushort %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(sbase)
+      : "memory");
+}
+
 // Wait until at most N vector-memory operations of this wave are in flight
 // (loads complete in order), drain LDS reads, then barrier the workgroup.
 template <int N>

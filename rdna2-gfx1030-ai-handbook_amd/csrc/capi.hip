@@ -25,6 +25,9 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // 32-bit byte offsets from its base.
 constexpr int64_t kStageK = 128;
 constexpr int64_t kMaxOperandBytes = int64_t(1) << 31;
+// Work items of one grouped (MoE) GEMM launch: 256 workgroups x 512 table
+// entries each.
+constexpr int64_t kMoeMaxItems = 131072;
 
 // An operand of `rows` rows (row stride s_row, element stride s_k) can be read
 // in place by the GEMM kernel.
@@ -916,6 +919,9 @@ extern "C" int qg_moe_grouped_gemm(const int8_t* a, int64_t a_sm, int64_t a_rows
   if (epilogue != QG_MOE_EPI_I32 && (!a_scale || !b_scale)) return hipErrorInvalidValue;
   if (epilogue == QG_MOE_EPI_SILU_MUL && n % 32 != 0) return hipErrorInvalidValue;
   if (epilogue == QG_MOE_EPI_ROUTE && (!row_weight || !row_slot)) return hipErrorInvalidValue;
+  // work items (tiles x 256-column tiles): each workgroup holds its share's
+  // table entries in LDS (launch_i8_moe_gemm checks the same bound)
+  if (tiles_max * ((n + 255) / 256) > kMoeMaxItems) return hipErrorInvalidValue;
   if (tiles_max == 0) return hipSuccess;
   qg::I8GemmArgs p{};
   p.a = a;

@@ -246,3 +246,23 @@ def test_moe_dispatch_qx_rejects_invalid_arguments(lib):
     assert call(xq=ctypes.c_void_p(4100)) == INVALID            # xq not 8-byte aligned
     assert call(xs=None) == INVALID
     assert call(rows_max=0) == INVALID                          # the dispatch's own checks come first
+
+
+def test_moe_grouped_gemm_rejects_plans_beyond_its_item_table(lib):
+    """The grouped GEMM keeps each workgroup's share of the work items
+    (tiles x 256-column tiles) in LDS: at most 131072 items per launch; one
+    more is refused before any HIP call; no tiles at all launch nothing."""
+    p = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+
+    def call(tiles_max, n, **kw):
+        args = dict(a=p, a_sm=256, a_rows=64, row_token=None, rows_max=64, k=256, w=p, w_sn=256,
+                    w_estride=256 * n, n=n, n_experts=1, tiles=p, tiles_max=tiles_max, a_scale=p, b_scale=p,
+                    row_weight=None, row_slot=None, epilogue=_lib.MOE_EPI_SILU_MUL, out=p, out_sm=n // 2,
+                    out_rows=64, stream=None)
+        args.update(kw)
+        return lib.qg_moe_grouped_gemm(*args.values())
+
+    assert call(131073, 256) == INVALID         # one column tile: 131073 items
+    assert call(65537, 512) == INVALID          # two column tiles: 131074 items
+    assert call(43691, 768) == INVALID          # three: 131073 items
+    assert call(0, 256) == 0                    # no tiles: nothing to launch

@@ -33,11 +33,12 @@
 //  * the linear block id is remapped so that each of the 8 XCDs (round-robin
 //    workgroup dispatch) walks one contiguous, GROUP_M-ordered range of tiles,
 //    keeping the A rows and W columns it shares in its own L2;
-//  * the per-row / per-column scales and the bias are fetched into registers
-//    before the K loop and parked in LDS for the epilogue, which is
-//    specialised at compile time (output dtype x order) and, for full tiles,
-//    stages the rounded tile through LDS so that HBM sees coalesced 16-byte
-//    row stores.
+//  * the per-row / per-column scales and the bias reach LDS before the K
+//    loop (the 4-wave kernel through registers; the ping-pong kernels by
+//    direct copies into one of two parameter buffers) for the epilogue, which
+//    is specialised at compile time (output dtype x order) and, for full
+//    tiles, stages the rounded tile through LDS so that HBM sees coalesced
+//    16-byte row stores.
 #include "qg_common.h"
 #include "qg_internal.h"
 
@@ -671,10 +672,11 @@ constexpr int pp_copies() { return (G::BM > G::BN ? G::BM : G::BN) / 32; }
 // offset of the row that its copy i fetches (W rows n0 + 8 (gw + 4 i) +
 // (l >> 3) for waves 0-3, A rows for waves 4-7), including the swizzled
 // chunk; a_base / w_base point at K = 0. park() runs in every wave once its
-// first copies, and every load it issued before the loop, have landed, and
-// before the barrier that opens the loop: it parks the epilogue parameters in
-// LDS. With `pre`, this wave's stage-0 copies (W(0) for X, A(0) for Y) were
-// already issued by pp_prefetch0 (during the previous tile's epilogue). On
+// first copies, and every copy it issued before them, have landed, and
+// before the barrier that opens the loop (the callers finish their epilogue
+// parameters there). With `pre`, this wave's stage-0 copies (W(0) for X,
+// A(0) for Y) were already issued by pp_prefetch0 (during the previous
+// tile's epilogue). On
 // return no copy is in flight and every wave has passed the barrier after the
 // last read of the rings, so each wave may stage its epilogue in its own part
 // of the rings at once (group X's epilogue overlaps group Y's last MFMAs).

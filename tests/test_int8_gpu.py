@@ -213,6 +213,12 @@ def test_int8_pingpong_edges_and_epilogues(cuda, m, n, k):
         else:
             ref = o.epilogue_f(acc_o, sa.numpy(), sb.numpy(), bv, out=out, fused=kw.get("rounding") == "fused")
         assert np.array_equal(_bits(got, out), _bits(ref, out)), (out, bias_dt, kw)
+    # one column scale for every column (its single value copied to each)
+    sb1 = sb[:1]
+    got = int8_gemm_dequant(ag, wg.T, sag, sb1.to(cuda), bias.to(torch.float16).to(cuda), out_dtype=torch.float16)
+    ref = o.epilogue_f(acc_o, sa.numpy(), np.full(n, sb1.numpy()[0], dtype=np.float32),
+                       bias.to(torch.float16).float().numpy(), out="f16")
+    assert np.array_equal(_bits(got, "f16"), _bits(ref, "f16")), "scalar column scale"
 
 
 def test_int8_extreme_values(cuda):

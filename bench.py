@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X quantized-weight GEMM hot path (one GPU).
 
-Workload (the W8A8 INT8 GEMM metric's chain): the
+Workload (benchmark configuration 1, the W8A8 INT8 GEMM metric's chain): the
 fused DiT-block INT8 GEMM chain at M = 4096 tokens, hidden 3072:
   QKV   = W8A8(x)              N = 9216,  K = 3072
   H     = GELU_tanh(W8A8(x))   N = 12288, K = 3072
@@ -19,11 +19,11 @@ around each GEMM launch on the chain's stream in instrumented chain rounds,
 alternated with the plain rounds that give ``value`` (the event records add
 about 4 % to a step).
 ``roofline_w4a16_decode`` is the metric's second half: the W4A16 decode kernel
-(M = 1) in GB/s against the 8 TB/s HBM peak, timed
+(benchmark configuration 2, M = 1) in GB/s against the 8 TB/s HBM peak, timed
 with events around graph replays of 120 launches over 12 rotated weight copies;
 its ``read_floor`` is qg_read_floor over the same byte count, rotated the same
 way (the plain-read floor of this box).
-``roofline_cfg0`` is the INT8 GEMM alone at BASELINE configuration 0, where
+``roofline_cfg0`` is the INT8 GEMM alone at benchmark configuration 0, where
 the metric's >= 60 % bar is quoted. ``secondary`` holds cfg0's quantizer,
 W4A16 M = 16 / 2048, the FP8 configuration 3, MoE (configuration 4), W4A8
 and the MOSS production INT8 shapes (M 1061, fp32 out).
@@ -133,7 +133,7 @@ class Chain:
 
 
 class Cfg0:
-    """BASELINE configuration 0 (M 4096, N = K = 3072, fp16 in / out, seed 0):
+    """Benchmark configuration 0 (M 4096, N = K = 3072, fp16 in / out, seed 0):
     the per-token quantizer and the INT8 GEMM with the order-F epilogue and
     bias, each launched through the C ABI on preallocated buffers."""
 
@@ -221,7 +221,7 @@ def _graph_time(torch, fn, launches, replays=4):
 
 
 def _w4_weights(torch, dev, copies):
-    """BASELINE configuration 2 weights (K 4096, N 14336, g128, uint4 storage with
+    """Benchmark configuration 2 weights (K 4096, N 14336, g128, uint4 storage with
     bf16 scales and packed uint4 zero points) and ``copies - 1`` clones."""
     from rdna2_ops import int4_weight_gemm_v07 as w4
     N, K, G = 14336, 4096, 128
@@ -233,7 +233,7 @@ def _w4_weights(torch, dev, copies):
 
 
 class DecodeW4:
-    """The W4A16 decode shapes of BASELINE configuration 2 (M = 1 and 16, bf16
+    """The W4A16 decode shapes of benchmark configuration 2 (M = 1 and 16, bf16
     activations and output). Each sample is one replay of a HIP graph of 120
     launches rotating over ``copies`` weight copies (366 MB, more than the
     256 MB MALL), so every launch streams its weights from HBM; the time per
@@ -332,7 +332,7 @@ class DecodeW4:
 
 
 def run_w4a16(torch, lib, _lib, dev, rows=(1, 16, 2048), copies=12):
-    """BASELINE configuration 2 at the given row counts, each the median of three
+    """Benchmark configuration 2 at the given row counts, each the median of three
     samples: decode rows (<= 16) through DecodeW4's rotated graphs, prefill
     (2048) over one weight with graph replays of 10 launches; for 2048 also the
     reference's default ``dequant`` method (this library's unpack to bf16, then
@@ -392,7 +392,7 @@ def run_w4a16(torch, lib, _lib, dev, rows=(1, 16, 2048), copies=12):
 
 
 def run_fp8(torch, lib, _lib, dev):
-    """e4m3 weights with per-channel absmax/448 scales,
+    """Benchmark configuration 3: e4m3 weights with per-channel absmax/448 scales,
     bf16 activations M 4096, K 3072, N 3072 and 12288, bf16 out. Timed per
     call of qg_fp8w_gemm: on these grids the 2-byte ping-pong GEMM with the fp8
     W stages converted exactly to bf16 in registers."""
@@ -439,7 +439,7 @@ def run_fp8(torch, lib, _lib, dev):
 
 
 def run_moe(torch, dev, iters=20):
-    """Secondary: BASELINE configuration 4, MoE prefill (4096 tokens, top-8 of 64
+    """Secondary: benchmark configuration 4, MoE prefill (4096 tokens, top-8 of 64
     experts, hidden 2048, F 768) through rdna2_ops.moe_int8: routing, dispatch,
     x quantization, grouped gate/up GEMM + SiLU*mul, h quantization, grouped
     down GEMM * routing weight, combine. Ops count the routed rows only
@@ -474,7 +474,7 @@ def run_moe(torch, dev, iters=20):
 
 
 def run_w4a8(torch, dev, iters=20):
-    """Secondary (no BASELINE configuration): W4A8 on the int8 MFMA,
+    """Secondary (no benchmark configuration): W4A8 on the int8 MFMA,
     int4_linear_a8 float output, on the cfg0 shape with g128 affine nk
     weights and on the reference's own check shape (M 1061, g32, kn).
     TOPS = 2 M N K per call; HIP events over `iters` back-to-back calls."""

@@ -47,12 +47,12 @@ enum qg_epilogue {
   QG_EPI_ORDER_EAGER = 2,     /* Kitchen eager order E: t = out(f32(acc)*(sa*sb));
                                  t = out(f32(t) + f32(out(bias))) (comfy_int8.py:128-143) */
   QG_EPI_GELU_TANH = 4        /* GELU(tanh approximation) in fp32 before the final
-                                 rounding (new) */
+                                 rounding (new; benchmark configuration 1) */
 };
 
 /* Rounding mode of the per-row INT8 quantizer. */
 enum qg_rounding {
-  QG_ROUND_HALF_EVEN = 0, /* q = rint(x / step)        (BASELINE: round-half-even) */
+  QG_ROUND_HALF_EVEN = 0, /* q = rint(x / step)        (round half to even) */
   QG_ROUND_HALF_AWAY = 1  /* q = floor(z+.5) | ceil(z-.5) (fp8_weight_gemm_v06.py:87-90) */
 };
 
@@ -224,7 +224,7 @@ int qg_w8a8_linear_noalloc(const void* x, int x_dtype, int64_t x_sm, int64_t m,
  * QG_W4_SIGNED_NIBBLES selects the reference PackedInt4 coordinates
  * (int4_weight_gemm_v07.py:20-82): q in [-8, 7] stored as q & 15, zero points
  * in the same signed coordinates. Without it nibbles and zero points are
- * unsigned uint4 (flags = QG_W4_ZEROS_PACKED,
+ * unsigned uint4 (benchmark configuration 2: flags = QG_W4_ZEROS_PACKED,
  * bf16 scales, G = 128).
  * Shape contract (int4_weight_gemm_v07.py:436-440): n, k > 0, k % G == 0,
  * n * k < 2^31.
@@ -319,7 +319,7 @@ int qg_fp8_decode(const uint8_t* w, int w_dtype, int64_t w_sn, int64_t w_sk,
  * reference's storage); bias NULL or [n] of bias_dtype.
  * Replaces: the fused path _fp8_linear of fp8_weight_gemm
  *   (fp8_weight_gemm_v06.py:49-73, :195-206), whose products and fp32
- *   accumulation it performs exactly; BASELINE configuration 3 adds the
+ *   accumulation it performs exactly; benchmark configuration 3 adds the
  *   per-channel scale (s = absmax / 448).
  * a: [m, k] QG_F16 / QG_BF16 with strides (a_sm, a_sk); w: [n, k] with strides
  * (w_sn, w_sk); out: [m, n] contiguous QG_F16 / QG_BF16 / QG_F32. Operands that
@@ -339,9 +339,9 @@ int qg_fp8w_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_sk, int64_t
                  size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
- * MoE prefill with grouped INT8 GEMMs.
+ * MoE prefill with grouped INT8 GEMMs (benchmark configuration 4).
  * No counterpart in the reference repository (it has no MoE kernel); the
- * stages follow BASELINE's CPU formulation: softmax + top-k routing, tokens
+ * stages follow the benchmark's CPU formulation: softmax + top-k routing, tokens
  * sorted and padded per expert, per-expert INT8 GEMMs with a SiLU * mul
  * epilogue, scatter-add with the routing weights.
  * ------------------------------------------------------------------------- */
@@ -396,7 +396,7 @@ int qg_moe_dispatch(const float* logits, int64_t l_sm, int64_t tokens, int n_exp
  * fp32 [tokens], bit-identical to qg_quant_rows_i8(x, QG_BF16, ...,
  * QG_ROUND_HALF_EVEN). hidden % 8 == 0 and hidden <= 2048 (one wave per token
  * holds its row); anything else returns hipErrorInvalidValue and the caller
- * runs qg_moe_dispatch and qg_quant_rows_i8. This build's own (BASELINE
+ * runs qg_moe_dispatch and qg_quant_rows_i8. This build's own (benchmark
  * configuration 4 has no counterpart in the reference): the quantization's
  * loads overlap the routing's latency-bound shuffles instead of a launch of
  * their own. */

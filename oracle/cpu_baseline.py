@@ -1,7 +1,7 @@
 """Reference torch CPU formulation of the hot path, timed as bench.py's
 ``cpu_baseline`` leg (test/measurement infrastructure only — never the product).
 
-W8A8 (cfg0 / cfg1), as restated in BASELINE's CPU-baseline plan:
+W8A8 (cfg0 / cfg1), as restated in the benchmark's CPU-baseline formulation:
   per-token quantize  amax -> /127 -> x/step -> round (half-even) -> clamp -> int8
   torch._int_mm       exact int32 on the CPU
   epilogue order F    f32(acc) * f32(sa*sw), + bias in fp32 (separate ops), GELU-tanh
@@ -86,9 +86,9 @@ def time_cfg1_chain(rows=4096, hidden=3072, threads=None, seconds=10.0, seed=1):
 
 
 def time_w4a16_decode(n=14336, k=4096, group=128, seconds=5.0, seed=2, threads=None):
-    """CPU formulation of the W4A16 decode (M = 1):
+    """CPU formulation of the W4A16 decode (benchmark configuration 2, M = 1):
     dequantise the uint4 weight (q - z) * s to fp32, F.linear in fp32, cast to
-    bf16 — as restated in BASELINE's CPU-baseline plan. Repeated for about
+    bf16 — as restated in the benchmark's CPU-baseline formulation. Repeated for about
     ``seconds``; returns (GB/s of the packed weight streamed, median seconds,
     threads, sample description)."""
     threads = threads or len(os.sched_getaffinity(0))

@@ -5,7 +5,7 @@ Restates, in numpy on the CPU:
     exponent 0 -> m * 2^-9, 0x7f / 0xff -> NaN, else (e + 120) << 23 | m << 20;
     e5m2 exponent 0 -> m * 2^-16, exponent 31 -> inf / NaN, else
     (e + 112) << 23 | m << 21; the sign bit on top;
-  * the BASELINE configuration-3 weight encoding: per output channel
+  * the weight encoding of benchmark configuration 3: per output channel
     s = absmax / 448, w / s saturated to +-448, round to nearest even e4m3fn;
   * the weight-only product y = (A @ decode(W)^T) * s[n] (+ bias) in float64;
     the reference's own formulation has s = 1 and fp16 activations
@@ -71,7 +71,7 @@ def encode_e4m3(x: np.ndarray) -> np.ndarray:
 
 
 def quantize_weight_per_channel(w: np.ndarray):
-    """s[n] = absmax_n / 448 (1 for a zero row),
+    """Benchmark configuration 3: s[n] = absmax_n / 448 (1 for a zero row),
     codes = e4m3fn(sat(w / s)). Returns (uint8 codes [N, K], fp32 s [N])."""
     w = np.asarray(w, dtype=F32)
     s = (np.abs(w).max(1) / F32(E4M3_MAX)).astype(F32)

@@ -6,7 +6,7 @@ Restates, in numpy on the CPU:
     quantisation with fp32 division and round-half-to-even, signed nibbles
     q & 15 with q in [-8, 7], int32 zero points in the same signed coordinates,
     "nk"/"kn" word layouts and "low"/"high" nibble order;
-  * the BASELINE configuration-2 storage (this build's definition of "uint4
+  * the uint4 storage of benchmark configuration 2 (this build's definition of "uint4
     packed 8 per int32, asymmetric, group 128, bf16 scales, uint4 zero
     points"): the same affine rule evaluated with the bf16-rounded scale,
     unsigned nibbles, low order, zero points packed 8 per int32 along groups;
@@ -110,9 +110,9 @@ def unpack_int4_ref(p, *, floating=True):
     return (centred.astype(F32) * p["scales"][..., None]).reshape(p["n"], p["k"]).astype(F32)
 
 
-# ----------------------------------------------------------------- BASELINE uint4 storage
+# ----------------------------------------------------------------- uint4 storage, packed zero points
 def pack_uint4_baseline(w, *, group_size=128):
-    """Asymmetric uint4 storage of BASELINE configuration 2.
+    """Asymmetric uint4 storage of benchmark configuration 2.
 
     Per [N, group]: lo = min(min x, 0), hi = max(max x, 0),
     s = bf16((hi - lo) / 15) (1 for an all-zero group), zu = clip(rint(-lo/s), 0, 15),

@@ -12,7 +12,7 @@ Restates, in numpy on the CPU:
     (rdna2-ops/rdna2_ops/comfy_int8.py:128-143): t = out(f32(acc) * (sa*sw));
     t = out(f32(t) + f32(out(bias)));
   * the per-row quantizer of fp8_weight_gemm_v06.py:76-92 (half away from zero)
-    and the BASELINE per-token rule (absmax / 127, round half to even);
+    and the per-token rule of the benchmark (absmax / 127, round half to even);
   * GELU tanh approximation in the operation order of ATen's CPU kernel.
 """
 from __future__ import annotations
@@ -203,7 +203,7 @@ def quant_rows(x, rounding="half_even"):
 
 def quantize_weight_per_channel(w, rounding="half_even"):
     """Symmetric per-output-channel int8 weight quantization (scale = absmax/127),
-    the BASELINE weight preparation; identical arithmetic to quant_rows."""
+    the benchmark's weight preparation; identical arithmetic to quant_rows."""
     return quant_rows(w, rounding)
 
 

@@ -1,6 +1,6 @@
 """Oracle for the MoE prefill grouped INT8 path (test infrastructure only).
 
-The reference repository has no MoE kernel; BASELINE configuration 4 defines
+The reference repository has no MoE kernel; benchmark configuration 4 defines
 the computation, and its CPU baseline is "route with softmax + top-8, then a
 per-expert _int_mm loop with a SiLU*mul epilogue, then scatter-add with the
 routing weights". This module restates that computation in numpy on the CPU,

@@ -1673,7 +1673,7 @@ hipError_t launch_i8_gemm_stages(const I8GemmArgs& p, hipStream_t stream) {
 
 hipError_t launch_i8_gemm(const I8GemmArgs& p, hipStream_t stream) {
   if (p.M == 0 || p.N == 0) return hipSuccess;
-  // 256x192 tiles tile every BASELINE shape into whole multiples of the 256
+  // 256x192 tiles tile every benchmark shape into whole multiples of the 256
   // CUs (4096x3072 -> 256 tiles, x9216 -> 768, x12288 -> 1024). Smaller
   // problems use 128x128 tiles so that more CUs get work.
   const long big = static_cast<long>(ceil_div(p.M, 256)) * ceil_div(p.N, 192);

@@ -1,4 +1,4 @@
-// MoE prefill routing, dispatch and combine on gfx950 (BASELINE configuration
+// MoE prefill routing, dispatch and combine on gfx950 (benchmark configuration
 // 4; the reference repository has no MoE kernel). The grouped INT8 GEMM that
 // runs between dispatch and combine is k_i8_moe_pp in int8_gemm.hip.
 //

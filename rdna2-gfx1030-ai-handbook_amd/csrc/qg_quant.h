@@ -4,7 +4,7 @@
 //   q = clamp(round(x / step), -127, 127)    (round of the IEEE quotient)
 // The step formula and the half-away rounding follow the reference's
 // in-tree quantizer rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:76-92; the
-// half-even mode is the BASELINE per-token rule (absmax/127, round-half-even).
+// half-even mode is the per-token rule of the benchmark (absmax/127, round-half-even).
 #pragma once
 #include "qg_common.h"
 #include "qg_internal.h"

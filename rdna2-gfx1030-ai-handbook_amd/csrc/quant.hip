@@ -16,7 +16,7 @@
 // rows take a two-pass kernel (pass 2 re-reads the row from L2).
 // The step formula and the half-away rounding follow the reference's
 // in-tree quantizer rdna2-ops/rdna2_ops/fp8_weight_gemm_v06.py:76-92; the
-// half-even mode is the BASELINE per-token rule (absmax/127, round-half-even).
+// half-even mode is the per-token rule of the benchmark (absmax/127, round-half-even).
 #include "qg_common.h"
 #include "qg_internal.h"
 #include "qg_quant.h"

@@ -126,7 +126,7 @@ __device__ __forceinline__ GroupRaw load_group(const W4Args& p, int n, int g) {
 }
 
 // UINT4: storage known at compile time to be bf16 scales, packed unsigned
-// zero points (the BASELINE format); otherwise resolved from p.flags.
+// zero points (the benchmark's uint4 format); otherwise resolved from p.flags.
 template <bool UINT4 = false>
 __device__ __forceinline__ GroupParams decode_group(const W4Args& p, GroupRaw raw, int n, int g,
                                                     float magic, float unit) {
@@ -793,7 +793,7 @@ hipError_t launch_skinny_t(const W4Args& p, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Single-row W4A16 decode (M = 1) on the BASELINE uint4 storage: unsigned
+// Single-row W4A16 decode (M = 1) on the benchmark's uint4 storage: unsigned
 // nibbles, low order, [N, K/8] words, bf16 scales, packed uint4 zero points,
 // group 128, bf16 activations, K a multiple of 512 up to 4096.
 //

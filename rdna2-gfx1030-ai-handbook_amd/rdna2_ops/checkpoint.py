@@ -190,7 +190,7 @@ class ResidentWeights:
 
 def w4_converter(*, group_size=128, symmetric=False, uint4=False, layout="nk", order="low"):
     """A ``ResidentWeights`` that packs floating [N, K] weights to W4 on their
-    device (pack_uint4 for the BASELINE uint4 storage, pack_int4 otherwise)."""
+    device (pack_uint4 for the unsigned uint4 storage with packed zero points, pack_int4 otherwise)."""
     from . import int4_weight_gemm_v07 as w4
 
     def prepare(w):

@@ -19,7 +19,7 @@ librdna2_qgemm.so (C ABI: include/qgemm.h):
 
 Extensions (defaults keep the reference's behaviour): bf16 activations (the
 output and bias then are bf16) and ``w_scale``, an fp32 per-output-channel
-scale applied to the fp32 accumulator before the bias (BASELINE configuration
+scale applied to the fp32 accumulator before the bias (benchmark configuration
 3: w_scale = absmax / 448, see ``quantize_weight_e4m3``).
 """
 from __future__ import annotations
@@ -75,7 +75,7 @@ def prepare_int8_weight(w):
 
 
 def quantize_weight_e4m3(w):
-    """BASELINE configuration 3 weight preparation (offline): per output channel
+    """Benchmark configuration 3 weight preparation (offline): per output channel
     s = absmax / 448 (1 for an all-zero row), codes = e4m3fn(clamp(w / s, +-448))
     with round-to-nearest-even. Returns (codes [N, K] float8_e4m3fn, s [N] fp32)."""
     if w.ndim != 2 or not w.is_floating_point():

@@ -26,7 +26,7 @@ group sums and fp32 group-scale order (bit-identical results);
 interfaces.
 
 Extensions (defaults keep the reference's behaviour): bf16 activations (the
-output and bias then are bf16), and the BASELINE configuration-2 storage
+output and bias then are bf16), and the uint4 storage of benchmark configuration 2
 ``pack_uint4`` — unsigned nibbles, bf16 scales, uint4 zero points packed 8 per
 int32 (PackedInt4 with ``signed=False, zeros_packed=True``).
 
@@ -50,7 +50,7 @@ class PackedInt4:
 
     ``signed`` / ``zeros_packed`` describe the storage coordinates: the
     reference format is signed=True, zeros_packed=False (int32 zero points);
-    the BASELINE uint4 format is signed=False, zeros_packed=True."""
+    the uint4 format (unsigned nibbles, packed zero points) is signed=False, zeros_packed=True."""
     data: torch.Tensor
     scales: torch.Tensor
     zeros: torch.Tensor
@@ -234,7 +234,7 @@ def pack_int4(w, *, group_size=64, symmetric=True, layout="nk", order="low"):
 
 
 def pack_uint4(w, *, group_size=128):
-    """BASELINE configuration-2 storage: asymmetric, unsigned nibbles (nk, low
+    """uint4 storage of benchmark configuration 2: asymmetric, unsigned nibbles (nk, low
     order), bf16 scales (the scale is rounded to bf16 before the codes are
     computed) and uint4 zero points packed 8 per int32 along the groups."""
     return _pack(w, group_size, False, "nk", "low", False, True, torch.bfloat16)
@@ -278,7 +278,7 @@ def unpack_int4(p, *, dtype=torch.float16):
 
 def _gemv1_applies(a, p):
     """Whether the C ABI serves this call with the single-row kernel
-    (k_w4_gemv1): one bf16 activation row, the BASELINE uint4 storage (nk, low
+    (k_w4_gemv1): one bf16 activation row, the benchmark's uint4 storage (nk, low
     order, bf16 scales, packed zero points), group 128, K a multiple of 512 up
     to 4096, 16-byte aligned weights and activations."""
     a = a if (a.stride(1) == 1 and a.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0) else a.contiguous()

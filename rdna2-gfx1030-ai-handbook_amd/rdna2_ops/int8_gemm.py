@@ -183,7 +183,7 @@ def w8a8_linear(x, weight, weight_scale, bias=None, *, out_dtype=None, activatio
 
     x: [..., K] fp32/fp16/bf16 with unit K stride. weight: int8 [N, K].
     weight_scale: fp32 [N] (or [N, 1]) or a one-element tensor.
-    rounding: "half_even" (BASELINE per-token rule) or "half_away" (the
+    rounding: "half_even" (per-token rule of the benchmark) or "half_away" (the
     reference's in-tree _quant_rows, fp8_weight_gemm_v06.py:87-90).
     out_dtype defaults to x.dtype.
 

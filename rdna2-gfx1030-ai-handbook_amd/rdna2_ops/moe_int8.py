@@ -1,7 +1,7 @@
 # SPDX-License-Identifier: Apache-2.0
-"""MoE prefill with grouped INT8 GEMMs on gfx950.
+"""MoE prefill with grouped INT8 GEMMs on gfx950 (benchmark configuration 4).
 
-The reference repository has no MoE operator; this module follows BASELINE's
+The reference repository has no MoE operator; this module follows the benchmark's
 formulation ("route with softmax + top-8, then a per-expert INT8 GEMM with a
 SiLU*mul epilogue, then scatter-add with the routing weights") on the same
 conventions as the rest of rdna2_ops: per-token INT8 activations (absmax /

@@ -3,7 +3,7 @@
 ``quantize_int8_rowwise`` has the call shape of Kitchen's
 ``eager.quantize_int8_rowwise`` (third-party comfy_kitchen 0.2.40, called at
 rdna2-ops/rdna2_ops/comfy_int8.py:122 and int8_gemm.py:255): it returns
-``(codes int8 [M, K], scale fp32 [M, 1])``. The arithmetic is the BASELINE
+``(codes int8 [M, K], scale fp32 [M, 1])``. The arithmetic is the benchmark's
 per-token rule, step = max(absmax / 127, 1e-20) and q = round_half_even(x / step)
 with IEEE division, clamped to [-127, 127]; ``rounding="half_away"`` selects the
 reference's in-tree Triton quantizer instead

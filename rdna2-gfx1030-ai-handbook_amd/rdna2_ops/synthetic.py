@@ -1,8 +1,8 @@
-"""Seeded synthetic inputs of the BASELINE configurations.
+"""Seeded synthetic inputs of the benchmark configurations.
 
 Every tensor is drawn on the CPU from ``torch.Generator().manual_seed(seed)`` in
 the fixed order written below, so a CPU checker and the GPU see identical bytes.
-BASELINE fixes cfg0's seed (0); seeds 1-4 of cfg1-cfg4 are this build's choice.
+The benchmark fixes cfg0's seed (0); seeds 1-4 of cfg1-cfg4 are this build's choice.
 There are no datasets or checkpoints: all data is synthetic.
 """
 from __future__ import annotations
@@ -20,7 +20,7 @@ class Cfg0:
 
 
 def cfg0(m=4096, n=3072, k=3072, seed=0) -> Cfg0:
-    """W8A8 INT8 linear."""
+    """W8A8 INT8 linear (benchmark configuration 0)."""
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(m, k, generator=g)
     outlier = torch.rand(m, k, generator=g) < 0.001
@@ -42,7 +42,7 @@ class Cfg1:
 
 
 def cfg1(m=4096, hidden=3072, seed=1) -> Cfg1:
-    """Fused DiT-block INT8 GEMM chain: QKV N=3H, MLP up
+    """Fused DiT-block INT8 GEMM chain (benchmark configuration 1): QKV N=3H, MLP up
     N=4H with GELU-tanh, MLP down K=4H -> N=H; same scheme as config 0."""
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(m, hidden, generator=g)
@@ -65,7 +65,7 @@ class Cfg4:
 
 
 def cfg4(tokens=4096, hidden=2048, experts=64, inter=768, top_k=8, seed=4) -> Cfg4:
-    """MoE prefill grouped INT8 GEMM: router logits and
+    """MoE prefill grouped INT8 GEMM (benchmark configuration 4): router logits and
     activations N(0, 1), expert weights N(0, 0.02), drawn in this order."""
     g = torch.Generator().manual_seed(seed)
     logits = torch.randn(tokens, experts, generator=g)

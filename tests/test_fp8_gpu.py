@@ -2,7 +2,7 @@
 
 Decoding is bit-exact for all 256 byte patterns (both the decode kernel and
 the in-register conversion of the fused GEMM). The fused GEMM is held to the
-BASELINE bar, |y - y64| <= 1e-2 * rms(y64) plus the output format's own
+1e-2 x RMS bar, |y - y64| <= 1e-2 * rms(y64) plus the output format's own
 rounding (half an ulp at |y64|), and to a tight bound: its products are exact
 and its fp32 accumulation adds at most a few ulps of sum |a w|. The int8
 method is bit-exact against the oracle's composition of its steps.
@@ -34,7 +34,7 @@ def check(y, y64, absdot, out_dtype, label):
     err = np.abs(got - y64)
     rms = float(np.sqrt(np.mean(y64 ** 2)))
     half_ulp = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 0.0}[out_dtype]
-    assert (err <= 1e-2 * rms + half_ulp * np.abs(y64) * 1.0001 + 1e-30).all(), f"{label}: BASELINE bar"
+    assert (err <= 1e-2 * rms + half_ulp * np.abs(y64) * 1.0001 + 1e-30).all(), f"{label}: 1e-2 x RMS bar"
     bound = max(half_ulp, 2.0 ** -24) * np.abs(y64) * 1.0001 + 2.0 ** -20 * absdot + 2.0 ** -24
     bad = err > bound
     assert not bad.any(), f"{label}: {bad.sum()} beyond one rounding, worst {err[bad].max()}"
@@ -227,7 +227,7 @@ def test_fused_wide_tiles_ragged(cuda, e5):
 
 @pytest.mark.parametrize("n", [3072, 12288])
 def test_cfg3_full_size(cuda, n):
-    """BASELINE configuration 3 at its real shape: M 4096, K 3072, e4m3
+    """Benchmark configuration 3 at its real shape: M 4096, K 3072, e4m3
     weights with per-channel absmax / 448 scales, bf16 activations and output.
     Every output (4096 x n) is checked against the oracle on the CPU."""
     case(f"cfg3 fp8 m4096 k3072 n{n}")

@@ -1,4 +1,4 @@
-"""HIP graph capture of the library's launches (BASELINE wrappers on torch's
+"""HIP graph capture of the library's launches (the benchmark-shape wrappers on torch's
 capture stream): the library issues no memset, allocation or
 synchronisation, so a captured W8A8 linear (quantizer + INT8 GEMM + fused
 epilogue), W4A16 decode, W4A16 prefill (unpack + split 2-byte GEMM) and MoE

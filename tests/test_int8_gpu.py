@@ -237,7 +237,7 @@ def test_int8_extreme_values(cuda):
 
 
 def test_cfg0_full_size_bit_exact(cuda):
-    """BASELINE config 0 at full size: quantize (half-even), int8 GEMM and
+    """Benchmark configuration 0 at full size: quantize (half-even), int8 GEMM and
     order-F fp16 epilogue all bit-exact against the oracle."""
     from rdna2_ops import synthetic
     from rdna2_ops.int8_gemm import int8_gemm_dequant, int8_matmul, w8a8_linear
@@ -262,7 +262,7 @@ def test_cfg0_full_size_bit_exact(cuda):
 
 @pytest.mark.parametrize("stage", ["qkv", "up_gelu", "down"])
 def test_cfg1_chain_stages(cuda, stage):
-    """BASELINE config 1 at full size, stage by stage (each stage is fed the
+    """Benchmark configuration 1 at full size, stage by stage (each stage is fed the
     GPU's own input so every stage is checked in isolation): int32 bit-exact,
     fp16 outputs bit-exact (QKV, down) or within the GELU tolerance (up)."""
     from rdna2_ops import synthetic
@@ -303,11 +303,11 @@ def test_cfg1_chain_stages(cuda, stage):
 
 
 def test_cfg1_chain_end_to_end(cuda):
-    """BASELINE config 1 end to end on the GPU (QKV, then MLP up + GELU-tanh,
+    """Benchmark configuration 1 end to end on the GPU (QKV, then MLP up + GELU-tanh,
     whose fp16 output feeds the down projection), against the oracle chain on
     all 4096 tokens. QKV is bit-exact. The down projection's input differs from the oracle's
     by at most one fp16 ulp (GELU through the hardware exp2 / reciprocal), so
-    the final output is held to the BASELINE bar (1e-2 x RMS plus half an fp16
+    the final output is held to the bar (1e-2 x RMS plus half an fp16
     ulp) and to RMS(error) <= 2e-3 x RMS."""
     from rdna2_ops import synthetic
     from rdna2_ops.int8_gemm import w8a8_linear
@@ -335,7 +335,7 @@ def test_cfg1_chain_end_to_end(cuda):
     exp = np.asarray(ref_y, np.float64)
     err = np.abs(got - exp)
     rms = float(np.sqrt(np.mean(exp ** 2)))
-    assert (err <= 1e-2 * rms + 2.0 ** -11 * np.abs(exp) * 1.0001).all(), "BASELINE bar"
+    assert (err <= 1e-2 * rms + 2.0 ** -11 * np.abs(exp) * 1.0001).all(), "1e-2 x RMS bar"
     assert float(np.sqrt(np.mean(err ** 2))) <= 2e-3 * rms
 
 

@@ -98,7 +98,7 @@ def test_w4a8_reference_check_shapes(cuda):
 
 
 def test_w4a8_prepared_and_uint4(cuda):
-    """dot4_prepared with the centred INT8 weights of unpack_int4; BASELINE
+    """dot4_prepared with the centred INT8 weights of unpack_int4; benchmark
     uint4 storage (bf16 scales, packed uint4 zero points)."""
     case("w4a8 prepared and uint4")
     p, c, s, a, sa, bias = make(cuda, 96, 160, 512, 64, seed=5)

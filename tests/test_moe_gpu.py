@@ -281,3 +281,72 @@ def test_moe_grouped_table_skips_and_output_strides(cuda):
         assert (bits[~written][:, :F] == -1).all(), f"silu pad {pad}: rows outside the tiles written"
         outs.append(bits[:, :F])
     assert np.array_equal(outs[0], outs[1])
+
+
+def test_moe_grouped_several_items_per_workgroup(cuda):
+    """More work items than workgroups (300 tiles of one column tile on the
+    256-workgroup grid): workgroups walk two candidates, invalid table entries
+    (no expert, an expert past n_experts) fall between valid ones, partial
+    tiles of 1-40 rows, A rows gathered through row_token (out-of-range
+    tokens clamped), so each workgroup's item table, row tokens and
+    alternating parameter buffers are used across items. int32 products and
+    the route epilogue bit-exact against the oracle; rows outside the valid
+    tiles untouched."""
+    from rdna2_ops import _lib
+    case("moe grouped GEMM, several items per workgroup")
+    rng = np.random.default_rng(11)
+    E, K, N, T, A_ROWS = 4, 128, 256, 300, 2048
+    M = 192 * T
+    a = rng.integers(-127, 128, (A_ROWS, K), dtype=np.int8)
+    w = rng.integers(-127, 128, (E, N, K), dtype=np.int8)
+    tok = rng.integers(0, A_ROWS, M).astype(np.int32)
+    tok[[5, 777, 192 * 40 + 3]] = [-5, A_ROWS + 9, A_ROWS]
+    src = np.clip(tok, 0, A_ROWS - 1)
+    sa = (rng.random(A_ROWS, dtype=np.float32) * 0.02 + 0.001).astype(np.float32)
+    sb = (rng.random((E, N), dtype=np.float32) * 0.02 + 0.001).astype(np.float32)
+    rw = rng.random(M, dtype=np.float32).astype(np.float32)
+    slot = rng.permutation(M).astype(np.int32)
+    tiles = np.zeros((T, 4), np.int32)
+    valid = []
+    for t in range(T):
+        e = t % E
+        if t % 7 == 3:
+            e = -1
+        elif t % 11 == 5:
+            e = E
+        m0 = 192 * t
+        m1 = m0 + 1 + (37 * t) % 40
+        tiles[t] = (e, m0, m1, 0)
+        if 0 <= e < E:
+            valid.append((e, m0, m1))
+    tiles[0, 3] = T
+    d = {k_: torch.from_numpy(v).to(cuda) for k_, v in
+         dict(a=a, w=w, tok=tok, sa=sa, sb=sb, rw=rw, slot=slot, tiles=tiles).items()}
+    P = _lib.ptr
+
+    def call(epi, out, with_scales):
+        _lib.check(_lib.library().qg_moe_grouped_gemm(
+            P(d["a"]), K, A_ROWS, P(d["tok"]), M, K, P(d["w"]), K, N * K, N, E, P(d["tiles"]), T,
+            P(d["sa"]) if with_scales else None, P(d["sb"]) if with_scales else None,
+            P(d["rw"]) if with_scales else None, P(d["slot"]) if with_scales else None,
+            epi, P(out), out.stride(0), out.shape[0], _lib.stream_of(d["a"])), "qg_moe_grouped_gemm")
+
+    out = torch.full((M, N), -7, dtype=torch.int32, device=cuda)
+    call(_lib.MOE_EPI_I32, out, False)
+    got = out.cpu().numpy()
+    exp = np.full((M, N), -7, np.int64)
+    for e, r0, r1 in valid:
+        exp[r0:r1] = o8.int8_matmul(a[src[r0:r1]], np.ascontiguousarray(w[e].T))
+    assert np.array_equal(got.astype(np.int64), exp)
+
+    buf = torch.full((M, N), -1, dtype=torch.int16, device=cuda)  # 0xFFFF: a bf16 NaN
+    call(_lib.MOE_EPI_ROUTE, buf.view(torch.bfloat16), True)
+    vals = buf.view(torch.bfloat16).float().cpu().numpy()
+    bits = buf.cpu().numpy()
+    hit = np.zeros(M, bool)
+    for e, r0, r1 in valid:
+        yv = om.down(a[src[r0:r1]], sa[src[r0:r1]], w[e], sb[e], rw[r0:r1])
+        dst = slot[r0:r1]
+        assert np.array_equal(vals[dst], yv), (e, r0, r1)
+        hit[dst] = True
+    assert (bits[~hit] == -1).all(), "rows without a valid routed row written"

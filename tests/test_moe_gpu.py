@@ -350,3 +350,26 @@ def test_moe_grouped_several_items_per_workgroup(cuda):
         assert np.array_equal(vals[dst], yv), (e, r0, r1)
         hit[dst] = True
     assert (bits[~hit] == -1).all(), "rows without a valid routed row written"
+
+
+@pytest.mark.parametrize("t,top_k,h,out_sm", [(37, 1, 64, 64), (37, 3, 200, 208), (50, 8, 2048, 2048),
+                                              (20, 12, 96, 96), (19, 5, 13, 13), (8, 8, 24, 40)])
+def test_moe_combine_slot_counts_and_row_widths(cuda, t, top_k, h, out_sm):
+    """qg_moe_combine alone: out[t] = bf16(sum over k of y[t, k]) in k order,
+    bit-exact against the oracle for 1-12 slots per token, rows of 13 columns
+    (one column per thread) and a padded output stride whose padding stays
+    untouched."""
+    from rdna2_ops import _lib
+    case(f"moe combine t{t} k{top_k} h{h} out_sm{out_sm}")
+    g = torch.Generator().manual_seed(t * 131 + top_k * 7 + h)
+    y = (torch.randn(t * top_k, h, generator=g) * torch.exp(torch.randn(t * top_k, 1, generator=g) * 2)).bfloat16()
+    out = torch.full((t, out_sm), -1, dtype=torch.int16, device=cuda)  # 0xFFFF: a bf16 NaN
+    yd = y.to(cuda)
+    _lib.check(_lib.library().qg_moe_combine(_lib.ptr(yd), t, top_k, h, _lib.ptr(out), out_sm,
+                                             _lib.stream_of(yd)), "qg_moe_combine")
+    torch.cuda.synchronize()
+    got = out.cpu()
+    exp = om.combine(bf16_np(y).reshape(t, top_k, h))
+    exp_bits = torch.from_numpy(np.ascontiguousarray(exp)).bfloat16().view(torch.int16)
+    assert torch.equal(got[:, :h], exp_bits)
+    assert (got[:, h:] == -1).all()
